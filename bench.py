@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Benchmark of the MoE forward hot path on one MI355X.
+
+Workload (BASELINE.json metric and configs[3]): DeepSeek-V3-shape FP8
+block-scale MoE layer, T=4096 tokens, E=256 experts, top-8, D=7168,
+I=2048, SwiGLU; e4m3 expert weights with fp32 128x128 scales, x bf16
+quantised 1x128 in the forward, bf16 gate and output.  Synthetic data
+(seeded on the GPU); all inputs resident in HBM before timing.
+
+A step = one full layer forward (routing, x quantisation, permutation,
+both grouped GEMMs, combine).  Prints ONE JSON line on stdout; progress
+goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "llm-sys-project_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE layer tokens/s + % fp8 MFMA peak (1 MI355X, DSV3 shape T=4096)"
+FP8_PEAK = 5.0e15       # dense fp8 MFMA, FLOP/s
+HBM_PEAK = 8.0e12       # bytes/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def moe_bytes(T, E_active, K, D, I):
+    """Algorithmic HBM bytes: (layer, up-projection kernel) per launch."""
+    w1 = E_active * (2 * I * D + (2 * I // 128) * (D // 128) * 4)
+    w2 = E_active * (D * I + (D // 128) * (I // 128) * 4)
+    layer = w1 + w2 + T * D * 2 + 256 * D * 2 + T * D * 2
+    P = T * K
+    up = w1 + T * D + T * (D // 128) * 4 + P * I + P * (I // 128) * 4
+    return layer, up
+
+
+def cpu_baseline(x, wg, w1q, w1s, w2q, w2s, K, n_tokens):
+    """The CPU oracle (restatement of tests/test_moe.cu:32-140 with the fp8
+    formats) on a sample of tokens of the same workload."""
+    import numpy as np
+    import torch
+
+    import oracle
+    rows = np.arange(n_tokens)
+    xs = x[:n_tokens].cpu().numpy().view(np.uint16)
+    wgn = wg.cpu().numpy().view(np.uint16)
+    idx, _ = oracle.moe_route(oracle.bf16_to_f32(xs), oracle.bf16_to_f32(wgn), K)
+    used = np.unique(idx)
+    wmap = np.zeros(wg.shape[0], np.int32)
+    wmap[used] = np.arange(len(used), dtype=np.int32)
+    sel = torch.from_numpy(used).cuda()
+    q1, s1 = w1q.index_select(0, sel).cpu().numpy(), w1s.index_select(0, sel).cpu().numpy()
+    q2, s2 = w2q.index_select(0, sel).cpu().numpy(), w2s.index_select(0, sel).cpu().numpy()
+    oracle.lib()
+    t0 = time.perf_counter()
+    oracle.moe_forward_fp8(xs, wgn, q1, s1, q2, s2, K, wmap=wmap)
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": len(rows) / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{len(rows)} tokens of the T=4096 DSV3 fp8 workload (routing, x/act "
+                      f"quantisation, {len(used)} experts dequantised, combine); {dt:.1f} s"}
+
+
+def dsa_bench(amdmoe, synth, iters=20):
+    """BASELINE DSA decode: B=64, H=128, Dc=512, Dp=64, S=2048 of 32768."""
+    import torch
+    Q, H, S, page, ctx = 64, 128, 2048, 64, 32768
+    sets = [synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=s) for s in (5, 6)]
+    cfg = amdmoe.dsa_config(Q, H, 512, 64, S, page, Q * ctx)
+    out = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
+    for st in sets:
+        qn, qp, cache, pt, lg, pps = st
+        amdmoe.dsa_decode_bf16_paged(qn, qp, cache, pt, lg, out, cfg, pps)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(iters):   # alternate two index sets: 302 MB > the 256 MB MALL
+        qn, qp, cache, pt, lg, pps = sets[i & 1]
+        amdmoe.dsa_decode_bf16_paged(qn, qp, cache, pt, lg, out, cfg, pps)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / iters
+    nbytes = Q * (S * 1152 + H * 576 * 2 + H * 512 * 2 + S * 4 + (ctx // page) * 4)
+    flops = Q * H * S * (2 * 576 + 2 * 512)
+    del sets
+    return {"us_per_call": round(us, 2), "queries_per_s": round(Q / (us * 1e-6), 1),
+            "hbm_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4),
+            "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--cpu-sample", type=int, default=4, help="tokens for the CPU baseline (0: skip)")
+    ap.add_argument("--skip-dsa", action="store_true")
+    ap.add_argument("--traffic", default=None,
+                    help="JSON file with measured up-projection HBM bytes per launch")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import amdmoe
+    import synth
+    torch.cuda.set_device(0)
+    T, E, K, D, I = args.tokens, 256, 8, 7168, 2048
+    log(f"[bench] generating DSV3 fp8 weights E={E} D={D} I={I}")
+    w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=1234)
+    x, wg = synth.dsv3_inputs(T, E, D, seed=99)
+    cfg = amdmoe.moe_config(T, E, K, D, I)
+    ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_FP8)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+
+    # active experts (for the algorithmic byte count)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amdmoe.moe_gate_bf16(x, wg, idx, wts, cfg)
+    torch.cuda.synchronize()
+    e_active = int(torch.unique(idx).numel())
+
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        amdmoe.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, cfg, ws=ws)
+    torch.cuda.synchronize()
+
+    log(f"[bench] timing {args.steps} steps")
+    stage = [amdmoe.StageEvents() for _ in range(args.steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(args.steps):
+        stage[i].arm()
+        amdmoe.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, cfg, ws=ws)
+    t1.record()
+    amdmoe.StageEvents.disarm()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    per_stage = {n: sum(s.stage_ms()[n] for s in stage) / args.steps for n in amdmoe.StageEvents.NAMES}
+    log("[bench] stage ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per_stage.items()))
+
+    flops = 6 * T * K * D * I
+    layer_bytes, up_bytes = moe_bytes(T, e_active, K, D, I)
+    up_ms = per_stage["gemm_up"]
+    achieved = up_bytes / (up_ms * 1e-3) / 1e9
+    traffic = None
+    if args.traffic and os.path.exists(args.traffic):
+        traffic = json.load(open(args.traffic)).get("gemm_up_bytes")
+    result = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {"workload": f"dsv3_fp8_blockscale_moe_T{T}", "T": T, "E": E, "K": K, "D": D,
+                   "I": I, "experts_active": e_active},
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "fp8_peak_frac": round(flops / (ms * 1e-3) / FP8_PEAK, 4),
+        "layer_hbm_frac": round(layer_bytes / (ms * 1e-3) / HBM_PEAK, 4),
+        "stage_ms": {k: round(v, 4) for k, v in per_stage.items()},
+        "roofline": {"kernel": "grouped_gemm_kernel<fp8, up> (GEMM1 + SwiGLU + requant)",
+                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),
+                     "traffic": traffic, "algorithmic_bytes": up_bytes},
+    }
+    if not args.skip_dsa:
+        log("[bench] DSA decode")
+        result["dsa_decode"] = dsa_bench(amdmoe, synth)
+    if args.cpu_sample > 0:
+        log(f"[bench] CPU baseline on {args.cpu_sample} tokens")
+        result["cpu_baseline"] = cpu_baseline(x, wg, w1q, w1s, w2q, w2s, K, args.cpu_sample)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,199 @@
+/*
+ * amdmoe.h -- C ABI of the MI355X (gfx950) MoE forward and DSA decode library.
+ *
+ * Plain C: POD structs, raw device pointers, sizes, a hipStream_t passed as
+ * void* (NULL = the null stream).  No torch types, no C++ in the signatures.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are DEVICE pointers owned by the caller, row-major,
+ *     laid out as the reference documents (kernels/moe/naive_moe.cuh:21-76,
+ *     kernels/dsa/naive_dsa.cuh:20-87).
+ *   - Every call is asynchronous on `stream`; none synchronises the host.
+ *   - Return 0 (AMDMOE_OK) on success, a positive AMDMOE_ERR_* code
+ *     otherwise; amdmoe_last_error() then holds a message (per host thread).
+ *     The reference aborts instead (utils/cuda_utils.cuh:13-21); the C++
+ *     drop-in header include/naive_moe.h restores that behaviour.
+ *   - `workspace` may be NULL: the library then uses its own per-device
+ *     workspace, grown on demand (that first call allocates).  A non-NULL
+ *     workspace must hold amdmoe_moe_workspace_bytes() bytes; calls that
+ *     share one workspace must be ordered on one stream.
+ *   - bf16 tensors are passed as uint16_t (bfloat16 bit patterns), fp8 as
+ *     uint8_t OCP e4m3 ("E4M3FN") codes.
+ */
+#ifndef AMDMOE_H
+#define AMDMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AMDMOE_OK 0
+#define AMDMOE_ERR_INVALID 1   /* bad argument / unsupported shape            */
+#define AMDMOE_ERR_HIP 2       /* a HIP runtime call or kernel launch failed   */
+#define AMDMOE_ERR_WORKSPACE 3 /* caller workspace smaller than required      */
+
+/* Same member order and types as the reference (naive_moe.cuh:9-15), so a
+ * positional aggregate initialiser {T, E, K, D, I} means the same thing. */
+typedef struct MoeConfig {
+    int num_tokens;       /* T */
+    int num_experts;      /* E */
+    int top_k;            /* K */
+    int hidden_dim;       /* D */
+    int intermediate_dim; /* I */
+} MoeConfig;
+
+/* Same member order and types as the reference (naive_dsa.cuh:9-17). */
+typedef struct DsaConfig {
+    int num_queries;         /* Q  */
+    int num_heads;           /* H  */
+    int head_dim_compressed; /* Dc */
+    int head_dim_positional; /* Dp */
+    int num_selected_kv;     /* S  */
+    int page_size;           /* P  */
+    int total_kv_tokens;     /* N  */
+} DsaConfig;
+
+/* Arithmetic of a forward call. */
+#define AMDMOE_DTYPE_F32 0      /* fp32 in/out, fp32 intermediates            */
+#define AMDMOE_DTYPE_BF16 1     /* bf16 x/W1/W2/y, fp32 gate, bf16 activation */
+#define AMDMOE_DTYPE_FP8 2      /* e4m3 block-scaled experts, bf16 x/gate/y   */
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* amdmoe_last_error(void);
+
+/* Library version string. */
+const char* amdmoe_version(void);
+
+/* ------------------------------------------------------------------ MoE */
+
+/* Bytes of device workspace a forward of `dtype` needs for `cfg`. */
+int amdmoe_moe_workspace_bytes(const MoeConfig* cfg, int dtype, size_t* bytes);
+
+/* Full MoE layer, fp32.  Replaces moe_forward (kernels/moe/naive_moe.cuh:74-76,
+ * kernels/moe/naive_moe.cu:400-471): x [T,D], Wg [E,D], W1 [E,2I,D] (gate rows
+ * 0..I-1, up rows I..2I-1), W2 [E,D,I]; y [T,D] is overwritten. */
+int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float* w1,
+                           const float* w2, float* y, const MoeConfig* cfg,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Full MoE layer, bf16 storage with fp32 accumulation (BASELINE medium-bf16
+ * and Mixtral configs; same layouts as moe_forward).  gate_weight is fp32,
+ * gate_bias fp32 [E] is added to the logits before the softmax (NULL = no
+ * bias, as in the reference).  y bf16 [T,D] is overwritten. */
+int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                            const uint16_t* w1, const uint16_t* w2, uint16_t* y,
+                            const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* Full MoE layer, FP8 block-scale (BASELINE DeepSeek-V3 config).
+ *   x bf16 [T,D] (quantised internally to e4m3 with one fp32 scale per token
+ *   per 128 columns); gate_weight bf16 [E,D];
+ *   w1 e4m3 [E,2I,D] with w1_scale fp32 [E,2I/128,D/128];
+ *   w2 e4m3 [E,D,I]  with w2_scale fp32 [E,D/128,I/128];
+ *   y bf16 [T,D] overwritten.  D and I must be multiples of 128. */
+int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
+                           const float* w1_scale, const uint8_t* w2, const float* w2_scale,
+                           uint16_t* y, const MoeConfig* cfg, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* --- stage entry points with the reference's semantics --- */
+
+/* Routing: replaces moe_gate (naive_moe.cuh:27-29, naive_moe.cu:341-355).
+ * expert_indices int32 [T,K] in the reference's slot order, expert_weights
+ * fp32 [T,K] (softmax probabilities of the chosen experts, renormalised). */
+int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_indices,
+                        float* expert_weights, const MoeConfig* cfg, void* stream);
+
+/* Routing for the bf16 layer: bf16 x, fp32 gate (+ optional fp32 bias [E]). */
+int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                          int* expert_indices, float* expert_weights, const MoeConfig* cfg,
+                          void* stream);
+
+/* Routing for the fp8 layer: bf16 x, bf16 gate, logits on bf16 MFMA. */
+int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
+                         float* expert_weights, const MoeConfig* cfg, void* stream);
+
+/* Per-expert gather: replaces moe_gather (naive_moe.cuh:38-41,
+ * naive_moe.cu:357-366).  Tokens routed to expert_id in ascending token
+ * order: gathered [cnt,D], token_map [cnt], *count (device int). */
+int amdmoe_moe_gather_f32(const float* x, const int* expert_indices, const float* expert_weights,
+                          int expert_id, float* gathered, int* token_map, int* count,
+                          const MoeConfig* cfg, void* stream);
+
+/* All-expert permutation (the batched form of moe_gather's index work):
+ * counts [E], offsets [E+1] (exclusive scan), sorted_token / sorted_slot
+ * [offsets[E]] = token id / flat slot t*K+k, experts ascending, tokens
+ * ascending within an expert (the reference gather order). */
+int amdmoe_moe_permute(const int* expert_indices, const MoeConfig* cfg, int* counts,
+                       int* offsets, int* sorted_token, int* sorted_slot, void* stream);
+
+/* C[M,N] = A[M,K] * B[K,N], row-major, B not transposed: replaces
+ * naive_gemm (naive_moe.cuh:44-45, naive_moe.cu:368-374). */
+int amdmoe_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                          void* stream);
+
+/* out[i] = silu(gate[i]) * up[i]: replaces swiglu (naive_moe.cuh:50-51,
+ * naive_moe.cu:376-382). */
+int amdmoe_swiglu_f32(const float* gate, const float* up, float* out, int n, void* stream);
+
+/* output[token_map[m], :] += w(token_map[m], expert_id) * expert_out[m, :]
+ * for m < count (host int): replaces moe_scatter (naive_moe.cuh:59-62,
+ * naive_moe.cu:384-395).  Accumulates; count == 0 is a no-op. */
+int amdmoe_moe_scatter_f32(const float* expert_out, const int* token_map,
+                           const float* expert_weights, const int* expert_indices, int expert_id,
+                           float* output, int count, const MoeConfig* cfg, void* stream);
+
+/* --- weight / activation formats (BASELINE fp8 layout) --- */
+
+/* Row quantisation, 1x128 blocks: scale = amax/448 (1 for an all-zero
+ * block), q = e4m3_rne_sat(x/scale).  x bf16 [rows, cols], q [rows, cols],
+ * scale [rows, cols/128]. */
+int amdmoe_quant_rows_fp8(const uint16_t* x, long rows, int cols, uint8_t* q, float* scale,
+                          void* stream);
+
+/* Weight quantisation, 128x128 blocks, with a per-block multiplier u:
+ * scale = u * amax / 448, q = e4m3_rne_sat(w/scale).  w fp32 [rows, cols],
+ * u fp32 [rows/128, cols/128], q [rows, cols], scale [rows/128, cols/128]. */
+int amdmoe_quant_weight_fp8(const float* w, long rows, int cols, const float* u, uint8_t* q,
+                            float* scale, void* stream);
+
+/* Instrumentation (no reference counterpart; the reference times whole
+ * calls with events on stream 0, utils/cuda_utils.cuh:27-50).  While
+ * `events` is non-NULL, each MoE forward records events[0..6] (hipEvent_t,
+ * owned by the caller) on its stream: [0] start, [1] after routing,
+ * [2] after x quantisation (fp8 only; otherwise recorded with [1]),
+ * [3] after the permutation, [4] after the up-projection GEMM, [5] after
+ * the down-projection GEMM, [6] after the combine.  Per host thread;
+ * NULL turns it off. */
+int amdmoe_set_stage_events(void** events);
+
+/* ------------------------------------------------------------------ DSA */
+
+/* Sparse MLA decode, fp32: replaces dsa_forward (naive_dsa.cuh:81-87,
+ * naive_dsa.cu:435-474).  q_nope [Q,H,Dc], q_pe [Q,H,Dp], kv_c [N,Dc],
+ * kv_p [N,Dp], v [N,Dc], sparse_indices [Q,S] (flat rows); out [Q,H,Dc]. */
+int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* kv_cache_compressed,
+                           const float* kv_cache_positional, const float* v_cache,
+                           const int* sparse_indices, float* output, const DsaConfig* cfg,
+                           void* stream);
+
+/* Sparse MLA decode, bf16, paged latent cache (BASELINE DSA config).
+ * cache bf16 [num_pages * page_size, Dc+Dp]: columns 0..Dc-1 are K_c and
+ * also V (MLA absorbed), Dc..Dc+Dp-1 are K_p.  page_table int32
+ * [Q, pages_per_seq]; logical_indices int32 [Q,S] are positions in the
+ * query's sequence, physical row = page_table[q][i/page]*page + i%page.
+ * q_nope bf16 [Q,H,Dc], q_pe bf16 [Q,H,Dp]; out bf16 [Q,H,Dc].
+ * Requires Dc == 512, Dp == 64, H a multiple of 16. */
+int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
+                                 const uint16_t* cache, const int* page_table,
+                                 const int* logical_indices, uint16_t* output,
+                                 const DsaConfig* cfg, int pages_per_seq, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AMDMOE_H */

@@ -1,0 +1,415 @@
+// C ABI of the library (include/amdmoe.h): argument validation, workspace
+// layout, and the forward orchestration.  A forward is a fixed sequence of
+// launches on the caller's stream with no host synchronisation and no
+// allocation when a workspace is supplied:
+//   route (R1) -> [fp8: quantise x 1x128] -> permute (R2)
+//   -> grouped GEMM up + SwiGLU (R3/R4) -> grouped GEMM down + weight (R5)
+//   -> combine (ascending-expert sum per token)
+// The reference's moe_forward (kernels/moe/naive_moe.cu:400-471) instead
+// loops over experts on the host with a blocking device-to-host copy per
+// expert and eight cudaMalloc/cudaFree pairs per call.
+#include "internal.hpp"
+
+#include <mutex>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace amdmoe {
+
+static thread_local char g_err[1024] = "";
+static thread_local hipEvent_t* g_stage_events = nullptr;
+
+// Records stage boundary `i` when instrumentation is on.
+static int mark(int i, hipStream_t st) {
+    if (g_stage_events) AMDMOE_HIP_TRY(hipEventRecord(g_stage_events[i], st));
+    return AMDMOE_OK;
+}
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+// ---------------------------------------------------------------- workspace
+struct MoeWs {
+    int* idx;
+    float* wts;
+    int* counts;
+    int* offsets;
+    int* num_tiles;
+    int4* tiles;
+    int* sorted_token;
+    int* sorted_slot;
+    uint8_t* xq;
+    float* xs;
+    uint8_t* act;
+    float* act_s;
+    uint8_t* ypair;
+    size_t total;
+};
+
+static int elem_size(int dtype) { return dtype == AMDMOE_DTYPE_F32 ? 4 : (dtype == AMDMOE_DTYPE_BF16 ? 2 : 1); }
+
+// Lays the workspace out from `base` (nullptr: sizes only).
+static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
+    MoeWs w{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t* {
+        uint8_t* p = base ? base + off : nullptr;
+        off += align_up(bytes ? bytes : 1, 256);
+        return p;
+    };
+    const size_t T = c.num_tokens, E = c.num_experts, K = c.top_k, D = c.hidden_dim,
+                 I = c.intermediate_dim;
+    const size_t P = T * K;
+    w.idx = (int*)take(4 * P);
+    w.wts = (float*)take(4 * P);
+    w.counts = (int*)take(4 * E);
+    w.offsets = (int*)take(4 * (E + 1));
+    w.num_tiles = (int*)take(4);
+    w.tiles = (int4*)take(16 * (size_t)max_mtiles((long)P, (int)E));
+    w.sorted_token = (int*)take(4 * P);
+    w.sorted_slot = (int*)take(4 * P);
+    if (dtype == AMDMOE_DTYPE_FP8) {
+        w.xq = take(T * D);
+        w.xs = (float*)take(4 * T * (D / 128));
+        w.act = take(P * I);
+        w.act_s = (float*)take(4 * P * (I / 128));
+        w.ypair = take(2 * P * D);
+    } else {
+        const size_t es = elem_size(dtype);
+        w.act = take(es * P * I);
+        w.ypair = take(es * P * D);
+    }
+    w.total = off;
+    return w;
+}
+
+// Per-device cached workspace for calls that pass workspace == NULL.
+struct CachedWs {
+    std::mutex m;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+static CachedWs g_cache[64];
+
+static int cached_workspace(size_t need, void** out) {
+    int dev = 0;
+    AMDMOE_HIP_TRY(hipGetDevice(&dev));
+    AMDMOE_CHECK_ARG(dev >= 0 && dev < 64, "device id %d out of range", dev);
+    CachedWs& c = g_cache[dev];
+    std::lock_guard<std::mutex> lk(c.m);
+    if (c.bytes < need) {
+        if (c.ptr) AMDMOE_HIP_TRY(hipFree(c.ptr));  // hipFree waits for pending work
+        c.ptr = nullptr;
+        c.bytes = 0;
+        size_t grow = align_up(need + need / 4, 1 << 20);
+        AMDMOE_HIP_TRY(hipMalloc(&c.ptr, grow));
+        c.bytes = grow;
+    }
+    *out = c.ptr;
+    return AMDMOE_OK;
+}
+
+// ---------------------------------------------------------------- checks
+static int check_cfg(const MoeConfig* cfg, int dtype) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    const MoeConfig& c = *cfg;
+    AMDMOE_CHECK_ARG(c.num_tokens >= 0, "num_tokens=%d < 0", c.num_tokens);
+    AMDMOE_CHECK_ARG(c.num_experts >= 1 && c.num_experts <= 8192, "num_experts=%d outside [1, 8192]", c.num_experts);
+    AMDMOE_CHECK_ARG(c.top_k >= 1 && c.top_k <= 64, "top_k=%d outside [1, 64]", c.top_k);
+    AMDMOE_CHECK_ARG(c.hidden_dim >= 1 && c.intermediate_dim >= 1, "hidden_dim=%d / intermediate_dim=%d must be positive", c.hidden_dim, c.intermediate_dim);
+    AMDMOE_CHECK_ARG((long)c.num_tokens * c.top_k < (1L << 30), "T*K=%ld too large", (long)c.num_tokens * c.top_k);
+    const int kq = dtype == AMDMOE_DTYPE_F32 ? 32 : (dtype == AMDMOE_DTYPE_BF16 ? 64 : 128);
+    AMDMOE_CHECK_ARG(c.hidden_dim % kq == 0 && c.intermediate_dim % kq == 0,
+                     "hidden_dim=%d and intermediate_dim=%d must be multiples of %d for this dtype",
+                     c.hidden_dim, c.intermediate_dim, kq);
+    return AMDMOE_OK;
+}
+
+static int resolve_ws(const MoeConfig& c, int dtype, void* workspace, size_t bytes, MoeWs* out) {
+    MoeWs sz = ws_layout(c, dtype, nullptr);
+    void* base = workspace;
+    if (base) {
+        AMDMOE_CHECK_ARG(((uintptr_t)base & 255) == 0, "workspace must be 256-byte aligned");
+        if (bytes < sz.total)
+            return set_error(AMDMOE_ERR_WORKSPACE, "workspace of %zu bytes < required %zu", bytes, sz.total);
+    } else {
+        int rc = cached_workspace(sz.total, &base);
+        if (rc) return rc;
+    }
+    *out = ws_layout(c, dtype, (uint8_t*)base);
+    return AMDMOE_OK;
+}
+
+#define TRY(...)                      \
+    do {                              \
+        int rc_ = (__VA_ARGS__);      \
+        if (rc_) return rc_;          \
+    } while (0)
+
+// Shared tail of every forward: permute, both grouped GEMMs, combine.
+static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t* a_x,
+                       const float* x_scale, const uint8_t* w1, const float* w1s,
+                       const uint8_t* w2, const float* w2s, void* y, hipStream_t st) {
+    const int T = c.num_tokens, E = c.num_experts, K = c.top_k, D = c.hidden_dim,
+              I = c.intermediate_dim;
+    const long P = (long)T * K;
+    const long mtiles = max_mtiles(P, E);
+    const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);
+    TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
+                       w.sorted_slot, w.tiles, w.num_tiles, st));
+    TRY(mark(3, st));
+    GemmArgs up{};
+    up.a = a_x;
+    up.a_row_bytes = (long)D * es;
+    up.a_map = w.sorted_token;
+    up.a_scale = x_scale;
+    up.b = w1;
+    up.b_expert_bytes = 2L * I * D * es;
+    up.b_row_bytes = (long)D * es;
+    up.b_scale = w1s;
+    up.b_rows = 2 * I;
+    up.K = D;
+    up.n_out = I;
+    up.tiles = w.tiles;
+    up.num_tiles = w.num_tiles;
+    up.n_tiles_n = (int)ceil_div(I, 128);
+    up.out = w.act;
+    up.out_scale = w.act_s;
+    TRY(launch_grouped_gemm(dt, MODE_UP, up, mtiles, st));
+    TRY(mark(4, st));
+    GemmArgs dn{};
+    dn.a = w.act;
+    dn.a_row_bytes = (long)I * es;
+    dn.a_scale = w.act_s;
+    dn.b = w2;
+    dn.b_expert_bytes = (long)D * I * es;
+    dn.b_row_bytes = (long)I * es;
+    dn.b_scale = w2s;
+    dn.b_rows = D;
+    dn.K = I;
+    dn.n_out = D;
+    dn.tiles = w.tiles;
+    dn.num_tiles = w.num_tiles;
+    dn.n_tiles_n = (int)ceil_div(D, 256);
+    dn.out = w.ypair;
+    dn.sorted_slot = w.sorted_slot;
+    dn.wts = w.wts;
+    TRY(launch_grouped_gemm(dt, MODE_DOWN, dn, mtiles, st));
+    TRY(mark(5, st));
+    TRY(launch_combine(dt == DT_F32 ? DT_F32 : DT_BF16, w.ypair, w.idx, T, K, E, D, y, st));
+    return mark(6, st);
+}
+
+}  // namespace amdmoe
+
+using namespace amdmoe;
+
+extern "C" {
+
+const char* amdmoe_last_error(void) { return g_err; }
+
+const char* amdmoe_version(void) { return "amdmoe 0.1 gfx950"; }
+
+int amdmoe_set_stage_events(void** events) {
+    g_stage_events = (hipEvent_t*)events;
+    return AMDMOE_OK;
+}
+
+int amdmoe_moe_workspace_bytes(const MoeConfig* cfg, int dtype, size_t* bytes) {
+    AMDMOE_CHECK_ARG(dtype >= AMDMOE_DTYPE_F32 && dtype <= AMDMOE_DTYPE_FP8, "bad dtype %d", dtype);
+    TRY(check_cfg(cfg, dtype));
+    AMDMOE_CHECK_ARG(bytes != nullptr, "bytes is NULL");
+    *bytes = ws_layout(*cfg, dtype, nullptr).total;
+    return AMDMOE_OK;
+}
+
+int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float* w1,
+                           const float* w2, float* y, const MoeConfig* cfg, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
+    const MoeConfig& c = *cfg;
+    if (c.num_tokens == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(x && gate_weight && w1 && w2 && y, "null tensor pointer");
+    hipStream_t st = (hipStream_t)stream;
+    MoeWs w;
+    TRY(resolve_ws(c, AMDMOE_DTYPE_F32, workspace, workspace_bytes, &w));
+    TRY(mark(0, st));
+    TRY(launch_route_exact<float, float>(x, gate_weight, nullptr, c.num_tokens, c.num_experts,
+                                         c.top_k, c.hidden_dim, w.idx, w.wts, st));
+    TRY(mark(1, st));
+    TRY(mark(2, st));
+    return moe_experts(DT_F32, c, w, (const uint8_t*)x, nullptr, (const uint8_t*)w1, nullptr,
+                       (const uint8_t*)w2, nullptr, y, st);
+}
+
+int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                            const uint16_t* w1, const uint16_t* w2, uint16_t* y,
+                            const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
+    const MoeConfig& c = *cfg;
+    if (c.num_tokens == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(x && gate_weight && w1 && w2 && y, "null tensor pointer");
+    hipStream_t st = (hipStream_t)stream;
+    MoeWs w;
+    TRY(resolve_ws(c, AMDMOE_DTYPE_BF16, workspace, workspace_bytes, &w));
+    TRY(mark(0, st));
+    TRY(launch_route_exact<uint16_t, float>(x, gate_weight, gate_bias, c.num_tokens,
+                                            c.num_experts, c.top_k, c.hidden_dim, w.idx, w.wts,
+                                            st));
+    TRY(mark(1, st));
+    TRY(mark(2, st));
+    return moe_experts(DT_BF16, c, w, (const uint8_t*)x, nullptr, (const uint8_t*)w1, nullptr,
+                       (const uint8_t*)w2, nullptr, y, st);
+}
+
+int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
+                           const float* w1_scale, const uint8_t* w2, const float* w2_scale,
+                           uint16_t* y, const MoeConfig* cfg, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_FP8));
+    const MoeConfig& c = *cfg;
+    if (c.num_tokens == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(x && gate_weight && w1 && w1_scale && w2 && w2_scale && y,
+                     "null tensor pointer");
+    hipStream_t st = (hipStream_t)stream;
+    MoeWs w;
+    TRY(resolve_ws(c, AMDMOE_DTYPE_FP8, workspace, workspace_bytes, &w));
+    TRY(mark(0, st));
+    if (route_mfma_supported(c.num_experts, c.hidden_dim))
+        TRY(launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
+                              w.idx, w.wts, st));
+    else
+        TRY(launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, c.num_tokens,
+                                                   c.num_experts, c.top_k, c.hidden_dim, w.idx,
+                                                   w.wts, st));
+    TRY(mark(1, st));
+    TRY(launch_quant_rows(x, c.num_tokens, c.hidden_dim, w.xq, w.xs, st));
+    TRY(mark(2, st));
+    return moe_experts(DT_FP8, c, w, w.xq, w.xs, w1, w1_scale, w2, w2_scale, y, st);
+}
+
+int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_indices,
+                        float* expert_weights, const MoeConfig* cfg, void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
+    if (cfg->num_tokens == 0) return AMDMOE_OK;
+    return launch_route_exact<float, float>(x, gate_weight, nullptr, cfg->num_tokens,
+                                            cfg->num_experts, cfg->top_k, cfg->hidden_dim,
+                                            expert_indices, expert_weights, (hipStream_t)stream);
+}
+
+int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                          int* expert_indices, float* expert_weights, const MoeConfig* cfg,
+                          void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
+    if (cfg->num_tokens == 0) return AMDMOE_OK;
+    return launch_route_exact<uint16_t, float>(x, gate_weight, gate_bias, cfg->num_tokens,
+                                               cfg->num_experts, cfg->top_k, cfg->hidden_dim,
+                                               expert_indices, expert_weights,
+                                               (hipStream_t)stream);
+}
+
+int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
+                         float* expert_weights, const MoeConfig* cfg, void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
+    if (cfg->num_tokens == 0) return AMDMOE_OK;
+    if (route_mfma_supported(cfg->num_experts, cfg->hidden_dim))
+        return launch_route_mfma(x, gate_weight, cfg->num_tokens, cfg->num_experts, cfg->top_k,
+                                 cfg->hidden_dim, expert_indices, expert_weights,
+                                 (hipStream_t)stream);
+    return launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, cfg->num_tokens,
+                                                  cfg->num_experts, cfg->top_k, cfg->hidden_dim,
+                                                  expert_indices, expert_weights,
+                                                  (hipStream_t)stream);
+}
+
+int amdmoe_moe_gather_f32(const float* x, const int* expert_indices, const float* expert_weights,
+                          int expert_id, float* gathered, int* token_map, int* count,
+                          const MoeConfig* cfg, void* stream) {
+    (void)expert_weights;  // unused, as in the reference (naive_moe.cu:358)
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
+    AMDMOE_CHECK_ARG(expert_id >= 0 && expert_id < cfg->num_experts, "expert_id=%d out of range", expert_id);
+    return launch_gather_one(x, expert_indices, cfg->num_tokens, cfg->top_k, cfg->num_experts,
+                             cfg->hidden_dim, expert_id, gathered, token_map, count,
+                             (hipStream_t)stream);
+}
+
+int amdmoe_moe_permute(const int* expert_indices, const MoeConfig* cfg, int* counts,
+                       int* offsets, int* sorted_token, int* sorted_slot, void* stream) {
+    AMDMOE_CHECK_ARG(cfg && cfg->num_experts >= 1 && cfg->top_k >= 1 && cfg->num_tokens >= 0,
+                     "bad MoeConfig");
+    const MoeConfig& c = *cfg;
+    // the tile table is not part of this entry's outputs: a private buffer
+    // of the cached workspace holds it
+    const long mt = max_mtiles((long)c.num_tokens * c.top_k, c.num_experts);
+    void* scratch = nullptr;
+    TRY(cached_workspace(align_up(16 * (size_t)(mt + 1), 256) + 256, &scratch));
+    int4* tiles = (int4*)scratch;
+    int* nt = (int*)((uint8_t*)scratch + align_up(16 * (size_t)(mt + 1), 256));
+    return launch_permute(expert_indices, c.num_tokens, c.top_k, c.num_experts, kMTile, counts,
+                          offsets, sorted_token, sorted_slot, tiles, nt, (hipStream_t)stream);
+}
+
+int amdmoe_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                          void* stream) {
+    AMDMOE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "negative GEMM size");
+    return launch_naive_gemm_f32(A, B, C, M, N, K, (hipStream_t)stream);
+}
+
+int amdmoe_swiglu_f32(const float* gate, const float* up, float* out, int n, void* stream) {
+    return launch_swiglu_f32(gate, up, out, n, (hipStream_t)stream);
+}
+
+int amdmoe_moe_scatter_f32(const float* expert_out, const int* token_map,
+                           const float* expert_weights, const int* expert_indices, int expert_id,
+                           float* output, int count, const MoeConfig* cfg, void* stream) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    return launch_scatter_f32(expert_out, token_map, expert_weights, expert_indices, expert_id,
+                              output, count, cfg->num_tokens, cfg->top_k, cfg->hidden_dim,
+                              (hipStream_t)stream);
+}
+
+int amdmoe_quant_rows_fp8(const uint16_t* x, long rows, int cols, uint8_t* q, float* scale,
+                          void* stream) {
+    AMDMOE_CHECK_ARG(rows >= 0, "rows < 0");
+    return launch_quant_rows(x, rows, cols, q, scale, (hipStream_t)stream);
+}
+
+int amdmoe_quant_weight_fp8(const float* w, long rows, int cols, const float* u, uint8_t* q,
+                            float* scale, void* stream) {
+    return launch_quant_weight(w, rows, cols, u, q, scale, (hipStream_t)stream);
+}
+
+int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* kv_cache_compressed,
+                           const float* kv_cache_positional, const float* v_cache,
+                           const int* sparse_indices, float* output, const DsaConfig* cfg,
+                           void* stream) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    const DsaConfig& c = *cfg;
+    AMDMOE_CHECK_ARG(c.num_queries >= 0 && c.num_heads >= 0 && c.head_dim_compressed >= 1 &&
+                         c.head_dim_positional >= 0 && c.num_selected_kv >= 1,
+                     "bad DsaConfig");
+    return launch_dsa_f32(q_nope, q_pe, kv_cache_compressed, kv_cache_positional, v_cache,
+                          sparse_indices, output, c.num_queries, c.num_heads,
+                          c.head_dim_compressed, c.head_dim_positional, c.num_selected_kv,
+                          c.total_kv_tokens, (hipStream_t)stream);
+}
+
+int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
+                                 const uint16_t* cache, const int* page_table,
+                                 const int* logical_indices, uint16_t* output,
+                                 const DsaConfig* cfg, int pages_per_seq, void* stream) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    const DsaConfig& c = *cfg;
+    return launch_dsa_bf16_paged(q_nope, q_pe, cache, page_table, logical_indices, output,
+                                 c.num_queries, c.num_heads, c.head_dim_compressed,
+                                 c.head_dim_positional, c.num_selected_kv, c.page_size,
+                                 pages_per_seq, (hipStream_t)stream);
+}
+
+}  // extern "C"

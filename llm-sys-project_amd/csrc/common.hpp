@@ -1,0 +1,123 @@
+// Shared device/host helpers for the gfx950 MoE + DSA library.
+//
+// Everything here is CDNA4 (gfx950) specific: 64-lane wavefronts, MFMA
+// builtins, the OCP fp8 conversion instruction.  There is no other target.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/amdmoe.h"
+
+namespace amdmoe {
+
+constexpr int kWave = 64;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------ status
+// Records a message for amdmoe_last_error() and returns the status code.
+int set_error(int code, const char* fmt, ...);
+
+#define AMDMOE_HIP_TRY(expr)                                                           \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return ::amdmoe::set_error(AMDMOE_ERR_HIP, "%s:%d: %s: %s", __FILE__,       \
+                                       __LINE__, #expr, hipGetErrorString(e_));        \
+    } while (0)
+
+#define AMDMOE_CHECK_ARG(cond, ...)                                                    \
+    do {                                                                               \
+        if (!(cond)) return ::amdmoe::set_error(AMDMOE_ERR_INVALID, __VA_ARGS__);      \
+    } while (0)
+
+// Launch check: a launch failure surfaces through hipGetLastError.
+#define AMDMOE_LAUNCH_CHECK()                                                          \
+    do {                                                                               \
+        hipError_t e_ = hipGetLastError();                                             \
+        if (e_ != hipSuccess)                                                          \
+            return ::amdmoe::set_error(AMDMOE_ERR_HIP, "%s:%d: kernel launch: %s",      \
+                                       __FILE__, __LINE__, hipGetErrorString(e_));     \
+    } while (0)
+
+// ------------------------------------------------------------------ formats
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+
+// Four floats -> four OCP e4m3 bytes (RNE).  Inputs are pre-clamped to
+// +-448 so the hardware conversion never sees an out-of-range value; the
+// result then equals round-to-nearest-even with saturation.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3x4(float a, float b, float c, float d) {
+    a = fminf(fmaxf(a, -448.0f), 448.0f);
+    b = fminf(fmaxf(b, -448.0f), 448.0f);
+    c = fminf(fmaxf(c, -448.0f), 448.0f);
+    d = fminf(fmaxf(d, -448.0f), 448.0f);
+    int v = 0;
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, v, false);
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
+    return (uint32_t)v;
+}
+
+// ------------------------------------------------------------------ MFMA
+// 16x16 output tiles.  Operand lane layout (A and B alike): lane l supplies
+// row/column (l & 15) and the K-slot group (l >> 4).  Output: lane l holds
+// C[4*(l>>4) + i][l & 15], i = 0..3.
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// OCP e4m3 x e4m3, K = 128, unit (E8M0 = 127) hardware scales.
+__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ------------------------------------------------------------------ wave ops
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Orders this wave's LDS writes before its subsequent LDS reads by other
+// lanes of the same wave (waits for the writes, fences the compiler).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// ------------------------------------------------------------------ host
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline long ceil_div(long a, long b) { return (a + b - 1) / b; }
+
+}  // namespace amdmoe

@@ -1,0 +1,78 @@
+// Declarations shared by the library's translation units (kernel launchers
+// and the grouped-GEMM argument block).  Not part of the public ABI.
+#pragma once
+
+#include "common.hpp"
+
+namespace amdmoe {
+
+enum { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2 };
+enum { MODE_UP = 0, MODE_DOWN = 1 };
+
+constexpr int kMTile = 128;  // rows of one grouped-GEMM M-tile
+
+struct GemmArgs {
+    const uint8_t* a;        // A base
+    long a_row_bytes;        // bytes per A row
+    const int* a_map;        // UP: sorted_token (A row of sorted position); DOWN: unused
+    const float* a_scale;    // fp8: [A rows][K/128]
+    const uint8_t* b;        // expert weights base
+    long b_expert_bytes;     // bytes per expert
+    long b_row_bytes;        // bytes per weight row (K * element size)
+    const float* b_scale;    // fp8: [E][b_rows/128][K/128]
+    int b_rows;              // weight rows per expert (2I or D)
+    int K;                   // reduction length in elements
+    int n_out;               // UP: I, DOWN: D
+    const int4* tiles;       // M-tiles {expert, first sorted row, rows, 0}
+    const int* num_tiles;    // device count of M-tiles
+    int n_tiles_n;           // N-tiles per M-tile
+    uint8_t* out;            // UP: act [P, I]; DOWN: ypair [T*K, D]
+    float* out_scale;        // UP fp8: act scales [P, I/128]
+    const int* sorted_slot;  // DOWN: flat slot t*K+k of each sorted row
+    const float* wts;        // DOWN: routing weights [T*K]
+};
+
+// moe_route.hip
+template <typename XT, typename GT>
+int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int E, int K, int D,
+                       int* idx, float* wts, hipStream_t st);
+bool route_mfma_supported(int E, int D);
+int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
+                      float* wts, hipStream_t st);
+
+// moe_permute.hip
+int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
+                   int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
+                   hipStream_t st);
+int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D, int expert,
+                      float* gathered, int* token_map, int* count, hipStream_t st);
+
+// moe_quant.hip
+int launch_quant_rows(const uint16_t* x, long rows, int cols, uint8_t* q, float* scale,
+                      hipStream_t st);
+int launch_quant_weight(const float* w, long rows, int cols, const float* u, uint8_t* q,
+                        float* scale, hipStream_t st);
+
+// moe_gemm.hip
+long max_mtiles(long P, int E);
+int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
+
+// moe_combine.hip
+int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,
+                   hipStream_t st);
+int launch_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                          hipStream_t st);
+int launch_swiglu_f32(const float* gate, const float* up, float* out, int n, hipStream_t st);
+int launch_scatter_f32(const float* expert_out, const int* token_map, const float* wts,
+                       const int* idx, int expert, float* out, int count, int T, int K, int D,
+                       hipStream_t st);
+
+// dsa.hip
+int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const float* kp,
+                   const float* v, const int* idx, float* out, int Q, int H, int Dc, int Dp, int S,
+                   int N, hipStream_t st);
+int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
+                          const int* page_table, const int* logical, uint16_t* out, int Q, int H,
+                          int Dc, int Dp, int S, int page, int pages_per_seq, hipStream_t st);
+
+}  // namespace amdmoe

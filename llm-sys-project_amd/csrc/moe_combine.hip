@@ -1,0 +1,183 @@
+// Combine and the reference's remaining elementwise / surface stages.
+//
+// combine_kernel: y[t,:] = sum over token t's routed slots, in ascending
+// expert order, of ypair[t*K+k,:] (already weighted by the down-projection
+// epilogue).  This is the reference's accumulation order
+// (tests/test_moe.cu:123-132: out starts at 0, experts ascending,
+// out += w*g2), so the fp32 path reproduces it exactly given the same
+// per-expert rows.
+//
+// naive_gemm / swiglu / moe_scatter keep the reference stage contracts
+// (kernels/moe/naive_moe.cuh:44-62) for callers that drive the stages
+// themselves; moe_forward does not use them.
+#include "internal.hpp"
+
+namespace amdmoe {
+
+template <typename PT> struct Vec8;
+template <> struct Vec8<float> {
+    static __device__ __forceinline__ void load(const float* p, float* v) {
+        f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+        for (int i = 0; i < 4; i++) { v[i] = a[i]; v[4 + i] = b[i]; }
+    }
+};
+template <> struct Vec8<uint16_t> {
+    static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
+        u32x4 a = *(const u32x4*)p;
+        for (int i = 0; i < 4; i++) {
+            v[2 * i] = __uint_as_float(a[i] << 16);
+            v[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+        }
+    }
+};
+
+template <typename PT, bool OUT_BF16>
+__global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypair,
+                                                      const int* __restrict__ idx, int T, int K,
+                                                      int E, int D, void* __restrict__ y) {
+    __shared__ int s_ord[64];
+    __shared__ int s_n;
+    const int t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        // valid first-occurrence slots, insertion-sorted by expert id
+        int n = 0;
+        int ek[64];
+        for (int k = 0; k < K; k++) {
+            int e = idx[(size_t)t * K + k];
+            if (e < 0 || e >= E) continue;
+            bool dup = false;
+            for (int j = 0; j < k; j++) dup |= idx[(size_t)t * K + j] == e;
+            if (dup) continue;
+            int p = n++;
+            while (p > 0 && ek[p - 1] > e) { ek[p] = ek[p - 1]; s_ord[p] = s_ord[p - 1]; p--; }
+            ek[p] = e;
+            s_ord[p] = k;
+        }
+        s_n = n;
+    }
+    __syncthreads();
+    const int n = s_n;
+    for (int c = threadIdx.x; c < D / 8; c += blockDim.x) {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < n; j++) {
+            float v[8];
+            Vec8<PT>::load(ypair + ((size_t)t * K + s_ord[j]) * D + 8 * c, v);
+            for (int i = 0; i < 8; i++) acc[i] = __fadd_rn(acc[i], v[i]);
+        }
+        if (OUT_BF16) {
+            u32x4 o;
+            for (int i = 0; i < 4; i++) o[i] = pack_bf16x2(acc[2 * i], acc[2 * i + 1]);
+            *(u32x4*)((uint16_t*)y + (size_t)t * D + 8 * c) = o;
+        } else {
+            float* dst = (float*)y + (size_t)t * D + 8 * c;
+            *(f32x4*)dst = (f32x4){acc[0], acc[1], acc[2], acc[3]};
+            *(f32x4*)(dst + 4) = (f32x4){acc[4], acc[5], acc[6], acc[7]};
+        }
+    }
+}
+
+int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,
+                   hipStream_t st) {
+    AMDMOE_CHECK_ARG(K <= 64 && D % 8 == 0, "combine: K=%d D=%d unsupported", K, D);
+    if (T == 0) return AMDMOE_OK;
+    if (dt == DT_F32)
+        hipLaunchKernelGGL((combine_kernel<float, false>), dim3(T), dim3(256), 0, st,
+                           (const float*)ypair, idx, T, K, E, D, y);
+    else
+        hipLaunchKernelGGL((combine_kernel<uint16_t, true>), dim3(T), dim3(256), 0, st,
+                           (const uint16_t*)ypair, idx, T, K, E, D, y);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+// ---------------------------------------------------------------- naive_gemm
+// C[M,N] = A[M,K] * B[K,N] (B row-major, not transposed): 64x64 output tile
+// per 256-thread block, 4x4 outputs per thread, K staged through LDS 16 at a
+// time.  Surface-only entry (the forward uses the grouped MFMA kernels).
+__global__ __launch_bounds__(256) void gemm_nn_f32_kernel(const float* __restrict__ A,
+                                                          const float* __restrict__ B,
+                                                          float* __restrict__ C, int M, int N,
+                                                          int K) {
+    __shared__ float As[16][65];
+    __shared__ float Bs[16][65];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        for (int j = threadIdx.x; j < 1024; j += 256) {
+            int r = j >> 4, c = j & 15;  // A tile 64 rows x 16 k
+            int gm = m0 + r, gk = k0 + c;
+            As[c][r] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.f;
+            int kr = j >> 6, nc = j & 63;  // B tile 16 k x 64 cols
+            int bk = k0 + kr, bn = n0 + nc;
+            Bs[kr][nc] = (bk < K && bn < N) ? B[(size_t)bk * N + bn] : 0.f;
+        }
+        __syncthreads();
+        for (int kk = 0; kk < 16; kk++)
+            for (int i = 0; i < 4; i++)
+                for (int j = 0; j < 4; j++) acc[i][j] += As[kk][ty * 4 + i] * Bs[kk][tx * 4 + j];
+        __syncthreads();
+    }
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) {
+            int gm = m0 + ty * 4 + i, gn = n0 + tx * 4 + j;
+            if (gm < M && gn < N) C[(size_t)gm * N + gn] = acc[i][j];
+        }
+}
+
+int launch_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                          hipStream_t st) {
+    if (M == 0 || N == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG((M + 63) / 64 <= 65535, "naive_gemm: M=%d too large", M);
+    hipLaunchKernelGGL(gemm_nn_f32_kernel, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, st,
+                       A, B, C, M, N, K);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+// ---------------------------------------------------------------- swiglu
+__global__ void swiglu_f32_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                  float* __restrict__ out, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        float x = g[i];
+        out[i] = x / (1.0f + expf(-x)) * u[i];
+    }
+}
+
+int launch_swiglu_f32(const float* gate, const float* up, float* out, int n, hipStream_t st) {
+    if (n <= 0) return AMDMOE_OK;
+    hipLaunchKernelGGL(swiglu_f32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, gate, up, out, n);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+// ---------------------------------------------------------------- scatter
+// output[token_map[m], :] += w * expert_out[m, :], w = weight of the first
+// slot of that token holding `expert` (naive_moe.cu:315-335).  A token
+// appears once per expert, so rows never collide and no atomics are needed.
+__global__ void scatter_f32_kernel(const float* __restrict__ eo, const int* __restrict__ tmap,
+                                   const float* __restrict__ wts, const int* __restrict__ idx,
+                                   int expert, float* __restrict__ out, int K, int D) {
+    const int m = blockIdx.y;
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= D) return;
+    const int t = tmap[m];
+    float w = 0.0f;
+    for (int k = 0; k < K; k++)
+        if (idx[(size_t)t * K + k] == expert) { w = wts[(size_t)t * K + k]; break; }
+    out[(size_t)t * D + d] += w * eo[(size_t)m * D + d];
+}
+
+int launch_scatter_f32(const float* expert_out, const int* token_map, const float* wts,
+                       const int* idx, int expert, float* out, int count, int T, int K, int D,
+                       hipStream_t st) {
+    if (count <= 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(count <= T && count <= 65535, "moe_scatter: count=%d out of range", count);
+    hipLaunchKernelGGL(scatter_f32_kernel, dim3((D + 255) / 256, count), dim3(256), 0, st,
+                       expert_out, token_map, wts, idx, expert, out, K, D);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+}  // namespace amdmoe

@@ -1,0 +1,180 @@
+// R2 -- token permutation: histogram, prefix sum, stable compaction into an
+// expert-sorted order, plus the M-tile table of the grouped GEMMs.
+//
+// Reference: moe_gather / gather_kernel (kernels/moe/naive_moe.cu:147-166,
+// 357-366; CPU tests/test_moe.cu:76-83): for each expert, one thread scans
+// idx[T,K] in ascending token order, lists a token once (first matching
+// slot), and the host syncs on the count before every expert.
+//
+// Here one launch serves every expert with no host round trip.  Workgroup e
+// (one per expert):
+//   1. builds the full expert histogram in LDS (order-independent counts),
+//   2. derives its own row offset = sum of counts of lower experts, and its
+//      M-tile offset = sum of ceil(count/BM) of lower experts,
+//   3. compacts the slots holding e in flat slot order t*K+k (= ascending
+//      token order) with a block-wide ballot prefix sum, so the output is
+//      deterministic and equals the reference gather order exactly,
+//   4. writes its M-tiles {expert, first row, rows}.
+// Work is O(E * T*K) slot reads, all L2-resident (T*K*4 bytes per expert),
+// in exchange for zero global atomics and zero inter-block ordering.
+#include "internal.hpp"
+
+namespace amdmoe {
+
+constexpr int kPermThreads = 1024;
+
+// Slot i = t*K + k counts for expert e = idx[i] only if no earlier slot of
+// the same token holds e (the reference's `break`).  Slots with e outside
+// [0,E) (the -1 left when K > E) count nowhere.
+__device__ __forceinline__ int slot_expert(const int* __restrict__ idx, int i, int K, int E) {
+    int e = idx[i];
+    if (e < 0 || e >= E) return -1;
+    int k = i % K;
+    for (int j = i - k; j < i; j++)
+        if (idx[j] == e) return -1;
+    return e;
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(
+    const int* __restrict__ idx, int T, int K, int E, int BM, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ sorted_token, int* __restrict__ sorted_slot,
+    int4* __restrict__ tiles, int* __restrict__ num_tiles) {
+    extern __shared__ int s_hist[];            // [E]
+    __shared__ int s_wave[kPermThreads / 64];  // per-wave totals
+    __shared__ int s_red[2];
+    const int e = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = T * K;
+
+    for (int j = tid; j < E; j += kPermThreads) s_hist[j] = 0;
+    __syncthreads();
+    for (int i = tid; i < P; i += kPermThreads) {
+        int v = slot_expert(idx, i, K, E);
+        if (v >= 0) atomicAdd(&s_hist[v], 1);
+    }
+    __syncthreads();
+
+    // offsets of this expert (rows and tiles) and, for block 0, the totals
+    int row_off = 0, tile_off = 0, rows_all = 0, tiles_all = 0;
+    for (int j = tid; j < E; j += kPermThreads) {
+        int c = s_hist[j];
+        int tl = (c + BM - 1) / BM;
+        if (j < e) { row_off += c; tile_off += tl; }
+        rows_all += c;
+        tiles_all += tl;
+    }
+    // block reduction of the four partial sums (wave shuffles + LDS)
+    auto block_sum = [&](int v) -> int {
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        __syncthreads();
+        if (lane == 0) s_wave[wave] = v;
+        __syncthreads();
+        if (tid == 0) {
+            int s = 0;
+            for (int w = 0; w < kPermThreads / 64; w++) s += s_wave[w];
+            s_red[0] = s;
+        }
+        __syncthreads();
+        return s_red[0];
+    };
+    row_off = block_sum(row_off);
+    tile_off = block_sum(tile_off);
+    rows_all = block_sum(rows_all);
+    tiles_all = block_sum(tiles_all);
+    const int cnt = s_hist[e];
+
+    // stable compaction, chunks of kPermThreads slots in flat order
+    int base = 0;
+    for (int c0 = 0; c0 < P; c0 += kPermThreads) {
+        int i = c0 + tid;
+        bool hit = i < P && slot_expert(idx, i, K, E) == e;
+        unsigned long long b = __ballot(hit);
+        int rank_in_wave = __popcll(b & ((1ull << lane) - 1ull));
+        __syncthreads();
+        if (lane == 0) s_wave[wave] = __popcll(b);
+        __syncthreads();
+        int before = 0, total = 0;
+        for (int w = 0; w < kPermThreads / 64; w++) {
+            int n = s_wave[w];
+            if (w < wave) before += n;
+            total += n;
+        }
+        if (hit) {
+            int pos = row_off + base + before + rank_in_wave;
+            sorted_token[pos] = i / K;
+            sorted_slot[pos] = i;
+        }
+        base += total;
+    }
+
+    for (int j = tid; j * BM < cnt; j += kPermThreads) {
+        int r0 = j * BM;
+        tiles[tile_off + j] = make_int4(e, row_off + r0, min(BM, cnt - r0), 0);
+    }
+    if (tid == 0) {
+        counts[e] = cnt;
+        offsets[e] = row_off;
+        if (e == 0) {
+            offsets[E] = rows_all;
+            *num_tiles = tiles_all;
+        }
+    }
+}
+
+int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
+                   int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
+                   hipStream_t st) {
+    size_t lds = sizeof(int) * (size_t)E;
+    AMDMOE_CHECK_ARG(lds <= 48 * 1024, "permute: E=%d too large", E);
+    hipLaunchKernelGGL(permute_kernel, dim3(E), dim3(kPermThreads), lds, st, idx, T, K, E, BM,
+                       counts, offsets, sorted_token, sorted_slot, tiles, num_tiles);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+// Single-expert gather with the reference's moe_gather contract
+// (naive_moe.cuh:31-41): one block compacts the expert's tokens in order,
+// then copies their rows.
+__global__ __launch_bounds__(kPermThreads) void gather_one_kernel(
+    const float* __restrict__ x, const int* __restrict__ idx, int T, int K, int E, int D,
+    int expert, float* __restrict__ gathered, int* __restrict__ token_map, int* __restrict__ count) {
+    __shared__ int s_wave[kPermThreads / 64];
+    __shared__ int s_cnt;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = T * K;
+    int base = 0;
+    for (int c0 = 0; c0 < P; c0 += kPermThreads) {
+        int i = c0 + tid;
+        bool hit = i < P && slot_expert(idx, i, K, E) == expert;
+        unsigned long long b = __ballot(hit);
+        int rank = __popcll(b & ((1ull << lane) - 1ull));
+        __syncthreads();
+        if (lane == 0) s_wave[wave] = __popcll(b);
+        __syncthreads();
+        int before = 0, total = 0;
+        for (int w = 0; w < kPermThreads / 64; w++) {
+            int n = s_wave[w];
+            if (w < wave) before += n;
+            total += n;
+        }
+        if (hit) token_map[base + before + rank] = i / K;
+        base += total;
+    }
+    if (tid == 0) { s_cnt = base; *count = base; }
+    __syncthreads();
+    const int cnt = s_cnt;
+    for (long j = tid; j < (long)cnt * D; j += kPermThreads) {
+        int m = (int)(j / D), d = (int)(j % D);
+        gathered[j] = x[(size_t)token_map[m] * D + d];
+    }
+}
+
+int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D, int expert,
+                      float* gathered, int* token_map, int* count, hipStream_t st) {
+    hipLaunchKernelGGL(gather_one_kernel, dim3(1), dim3(kPermThreads), 0, st, x, idx, T, K, E, D,
+                       expert, gathered, token_map, count);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+}  // namespace amdmoe

@@ -1,0 +1,78 @@
+"""Synthetic inputs of the BASELINE workloads, generated on the GPU.
+
+torch supplies device memory and seeded normals (plumbing); the fp8 block
+quantisation of the expert weights runs through the library's own HIP
+kernel (amdmoe_quant_weight_fp8).  Shapes and distributions:
+  - DeepSeek-V3 fp8 layer: W1 [E,2I,D], W2 [E,D,I] ~ N(0, 1/fan_in), e4m3
+    with fp32 128x128 scales u*amax/448, u ~ U(0.5, 2); x ~ N(0,1) bf16;
+    Wg ~ N(0, 1/D) bf16.
+  - Mixtral / medium bf16 layer: bf16 x ~ N(0,1), bf16 W ~ N(0, 1/fan_in),
+    fp32 gate ~ N(0, 1/D); optional per-expert logit bias ~ N(0, 0.5^2).
+  - DSA decode: bf16 latent cache ~ N(0,1) in pages, page table a random
+    permutation of physical pages, indices uniform without replacement.
+"""
+import torch
+
+import amdmoe
+
+
+def _gen(seed, device="cuda"):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def dsv3_weights(E, D, I, seed=1234, device="cuda"):
+    """fp8 block-scale expert weights, built one expert at a time."""
+    g = _gen(seed, device)
+    w1q = torch.empty((E, 2 * I, D), dtype=torch.uint8, device=device)
+    w2q = torch.empty((E, D, I), dtype=torch.uint8, device=device)
+    w1s = torch.empty((E, 2 * I // 128, D // 128), dtype=torch.float32, device=device)
+    w2s = torch.empty((E, D // 128, I // 128), dtype=torch.float32, device=device)
+    for e in range(E):
+        w = torch.randn((2 * I, D), generator=g, device=device) * (1.0 / D ** 0.5)
+        u = torch.rand((2 * I // 128, D // 128), generator=g, device=device) * 1.5 + 0.5
+        amdmoe.quant_weight_fp8(w, u, w1q[e], w1s[e])
+        w = torch.randn((D, I), generator=g, device=device) * (1.0 / I ** 0.5)
+        u = torch.rand((D // 128, I // 128), generator=g, device=device) * 1.5 + 0.5
+        amdmoe.quant_weight_fp8(w, u, w2q[e], w2s[e])
+        del w, u
+    torch.cuda.synchronize()
+    return w1q, w1s, w2q, w2s
+
+
+def dsv3_inputs(T, E, D, seed=99, device="cuda"):
+    """x bf16 [T,D] ~ N(0,1) and gate bf16 [E,D] ~ N(0, 1/D), as int16 bit views."""
+    g = _gen(seed, device)
+    x = torch.randn((T, D), generator=g, device=device).to(torch.bfloat16)
+    wg = (torch.randn((E, D), generator=g, device=device) * (1.0 / D ** 0.5)).to(torch.bfloat16)
+    return x.view(torch.int16), wg.view(torch.int16)
+
+
+def bf16_layer(T, E, D, I, seed=7, bias=False, device="cuda"):
+    """bf16 x, W1, W2 (int16 bit views), fp32 gate and optional fp32 bias."""
+    g = _gen(seed, device)
+    x = torch.randn((T, D), generator=g, device=device).to(torch.bfloat16)
+    wg = torch.randn((E, D), generator=g, device=device) * (1.0 / D ** 0.5)
+    w1 = (torch.randn((E, 2 * I, D), generator=g, device=device) * (1.0 / D ** 0.5)).to(torch.bfloat16)
+    w2 = (torch.randn((E, D, I), generator=g, device=device) * (1.0 / I ** 0.5)).to(torch.bfloat16)
+    b = torch.randn((E,), generator=g, device=device) * 0.5 if bias else None
+    return x.view(torch.int16), wg, b, w1.view(torch.int16), w2.view(torch.int16)
+
+
+def dsa_paged(Q, H, Dc, Dp, S, page, ctx, seed=5, device="cuda"):
+    """Paged bf16 latent cache and per-query logical indices.
+
+    Each query owns ctx tokens = ctx/page pages; the page table maps them to
+    a random permutation of all physical pages; each query selects S
+    distinct logical positions (unsorted)."""
+    g = _gen(seed, device)
+    pps = ctx // page
+    n_pages = Q * pps
+    cache = torch.randn((n_pages * page, Dc + Dp), generator=g, device=device).to(torch.bfloat16)
+    pt = torch.randperm(n_pages, generator=g, device=device).to(torch.int32).reshape(Q, pps)
+    logical = torch.stack([torch.randperm(ctx, generator=g, device=device)[:S] for _ in range(Q)])
+    logical = logical.to(torch.int32).contiguous()
+    qn = torch.randn((Q, H, Dc), generator=g, device=device).to(torch.bfloat16)
+    qp = torch.randn((Q, H, Dp), generator=g, device=device).to(torch.bfloat16)
+    return (qn.view(torch.int16), qp.view(torch.int16), cache.view(torch.int16), pt, logical, pps)

@@ -1,0 +1,296 @@
+"""numpy front-end for the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
+by bench.py's cpu_baseline leg, as the checker.  The product library never
+imports it and has no CPU fallback.
+
+Every function mirrors one C function of oracle.c, which cites the reference
+file:line it restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_L, _I, _F = ctypes.c_long, ctypes.c_int, ctypes.c_float
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "orc_srand": (None, [ctypes.c_uint]),
+            "orc_random_fill": (None, [_f32p, _L, _F, _F]),
+            "orc_gen_sparse_indices": (None, [_i32p, _I, _I, _I, _I]),
+            "orc_max_abs_error": (_F, [_f32p, _f32p, _L]),
+            "orc_mean_abs_error": (_F, [_f32p, _f32p, _L]),
+            "orc_f32_to_bf16_array": (None, [_f32p, _u16p, _L]),
+            "orc_bf16_to_f32_array": (None, [_u16p, _f32p, _L]),
+            "orc_e4m3_to_f32_array": (None, [_u8p, _f32p, _L]),
+            "orc_f32_to_e4m3": (ctypes.c_uint8, [_F]),
+            "orc_quant_rows_1x128": (None, [_f32p, _L, _I, _u8p, _f32p]),
+            "orc_quant_weight_128x128": (None, [_f32p, _I, _I, _f32p, _u8p, _f32p]),
+            "orc_softmax": (None, [_f32p, _I]),
+            "orc_topk_row": (None, [_f32p, _I, _I, _i32p, _f32p]),
+            "orc_moe_route": (None, [_f32p, _f32p, ctypes.c_void_p, _I, _I, _I, _I,
+                                     _i32p, _f32p, ctypes.c_void_p, ctypes.c_void_p]),
+            "orc_moe_permute": (None, [_i32p, _I, _I, _I, _i32p, _i32p, _i32p, _i32p]),
+            "orc_moe_forward_f32": (None, [_f32p, _f32p, _f32p, _f32p, ctypes.c_void_p,
+                                           _I, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
+            "orc_moe_forward_bf16": (None, [_u16p, _f32p, _u16p, _u16p, ctypes.c_void_p,
+                                            _I, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
+            "orc_dequant_weight_128x128": (None, [_u8p, _f32p, _I, _I, _f32p]),
+            "orc_moe_forward_fp8": (None, [_u16p, _I, _u16p, _u8p, _f32p, _u8p, _f32p,
+                                           ctypes.c_void_p, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
+            "orc_dsa_forward_f32": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _f32p,
+                                           _I, _I, _I, _I, _I]),
+            "orc_dsa_translate": (None, [_i32p, _i32p, _I, _I, _I, _I, _i32p]),
+            "orc_dsa_decode_bf16_paged": (None, [_u16p, _u16p, _u16p, _i32p, _i32p, _f32p,
+                                                 _I, _I, _I, _I, _I, _I, _I]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _opt(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- generators
+def srand(seed):
+    lib().orc_srand(seed)
+
+
+def random_fill(n, lo, hi):
+    """utils/cuda_utils.cuh:56-60 on the current glibc rand() stream."""
+    out = np.empty(n, np.float32)
+    lib().orc_random_fill(out, n, lo, hi)
+    return out
+
+
+def gen_sparse_indices(Q, S, N, sort_rows=True):
+    """tests/test_dsa.cu:73-85 (sort_rows=False keeps the draw order)."""
+    out = np.empty(Q * S, np.int32)
+    lib().orc_gen_sparse_indices(out, Q, S, N, int(sort_rows))
+    return out.reshape(Q, S)
+
+
+def reference_moe_inputs(T, E, K, D, I, seed=42):
+    """Inputs of tests/test_moe.cu:151-164 (srand(seed); x, Wg, W1, W2)."""
+    srand(seed)
+    x = random_fill(T * D, -0.5, 0.5).reshape(T, D)
+    wg = random_fill(E * D, -0.5, 0.5).reshape(E, D)
+    w1 = random_fill(E * 2 * I * D, -0.1, 0.1).reshape(E, 2 * I, D)
+    w2 = random_fill(E * D * I, -0.1, 0.1).reshape(E, D, I)
+    return x, wg, w1, w2
+
+
+def reference_dsa_inputs(Q, H, Dc, Dp, S, P, N, seed=42):
+    """Inputs of tests/test_dsa.cu:101-115."""
+    srand(seed)
+    qn = random_fill(Q * H * Dc, -0.3, 0.3).reshape(Q, H, Dc)
+    qp = random_fill(Q * H * Dp, -0.3, 0.3).reshape(Q, H, Dp)
+    kc = random_fill(N * Dc, -0.3, 0.3).reshape(N, Dc)
+    kp = random_fill(N * Dp, -0.3, 0.3).reshape(N, Dp)
+    v = random_fill(N * Dc, -0.3, 0.3).reshape(N, Dc)
+    idx = gen_sparse_indices(Q, S, N, True)
+    return qn, qp, kc, kp, v, idx
+
+
+# ---------------------------------------------------------------- formats
+def f32_to_bf16(a):
+    a = _c(a, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_f32_to_bf16_array(a.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+def bf16_to_f32(a):
+    a = _c(a, np.uint16)
+    out = np.empty(a.shape, np.float32)
+    lib().orc_bf16_to_f32_array(a.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+def e4m3_to_f32(a):
+    a = _c(a, np.uint8)
+    out = np.empty(a.shape, np.float32)
+    lib().orc_e4m3_to_f32_array(a.reshape(-1), out.reshape(-1), a.size)
+    return out
+
+
+def f32_to_e4m3_scalar(v):
+    return int(lib().orc_f32_to_e4m3(float(v)))
+
+
+def quant_rows_1x128(x):
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.uint8)
+    s = np.empty((rows, cols // 128), np.float32)
+    lib().orc_quant_rows_1x128(x, rows, cols, q, s)
+    return q, s
+
+
+def quant_weight_128x128(w, u):
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.uint8)
+    s = np.empty((rows // 128, cols // 128), np.float32)
+    lib().orc_quant_weight_128x128(w, rows, cols, _c(u, np.float32), q, s)
+    return q, s
+
+
+def dequant_weight_128x128(q, s):
+    q = _c(q, np.uint8)
+    rows, cols = q.shape
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_dequant_weight_128x128(q, _c(s, np.float32), rows, cols, out)
+    return out
+
+
+# ---------------------------------------------------------------- MoE
+def softmax(row):
+    r = _c(row, np.float32).copy()
+    lib().orc_softmax(r, r.size)
+    return r
+
+
+def topk_row(p, K):
+    p = _c(p, np.float32)
+    idx = np.empty(K, np.int32)
+    wt = np.empty(K, np.float32)
+    lib().orc_topk_row(p, p.size, K, idx, wt)
+    return idx, wt
+
+
+def moe_route(x, wg, K, bias=None, want_probs=False):
+    x = _c(x, np.float32)
+    wg = _c(wg, np.float32)
+    T, D = x.shape
+    E = wg.shape[0]
+    idx = np.empty((T, K), np.int32)
+    wts = np.empty((T, K), np.float32)
+    logits = np.empty((T, E), np.float32)
+    probs = np.empty((T, E), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().orc_moe_route(x, wg, _opt(b), T, E, K, D, idx, wts, _opt(logits), _opt(probs))
+    if want_probs:
+        return idx, wts, logits, probs
+    return idx, wts
+
+
+def moe_permute(idx, E):
+    idx = _c(idx, np.int32)
+    T, K = idx.shape
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E + 1, np.int32)
+    st = np.full(T * K, -1, np.int32)
+    ss = np.full(T * K, -1, np.int32)
+    lib().orc_moe_permute(idx, T, K, E, counts, offsets, st, ss)
+    n = int(offsets[E])
+    return counts, offsets, st[:n], ss[:n]
+
+
+def moe_forward_f32(x, wg, w1, w2, K, bias=None):
+    x, wg, w1, w2 = (_c(a, np.float32) for a in (x, wg, w1, w2))
+    T, D = x.shape
+    E = wg.shape[0]
+    I = w1.shape[1] // 2
+    idx = np.empty((T, K), np.int32)
+    wts = np.empty((T, K), np.float32)
+    y = np.empty((T, D), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().orc_moe_forward_f32(x, wg, w1, w2, _opt(b), T, E, K, D, I, idx, wts, y)
+    return idx, wts, y
+
+
+def moe_forward_bf16(x_bf16, wg_f32, w1_bf16, w2_bf16, K, bias=None):
+    x, w1, w2 = (_c(a, np.uint16) for a in (x_bf16, w1_bf16, w2_bf16))
+    wg = _c(wg_f32, np.float32)
+    T, D = x.shape
+    E = wg.shape[0]
+    I = w1.shape[1] // 2
+    idx = np.empty((T, K), np.int32)
+    wts = np.empty((T, K), np.float32)
+    y = np.empty((T, D), np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().orc_moe_forward_bf16(x, wg, w1, w2, _opt(b), T, E, K, D, I, idx, wts, y)
+    return idx, wts, y
+
+
+def moe_forward_fp8(x_bf16_rows, wg_bf16, w1q, w1s, w2q, w2s, K, wmap=None):
+    """wmap[e] = slot of expert e in the weight arrays (None: identity)."""
+    x = _c(x_bf16_rows, np.uint16)
+    wg = _c(wg_bf16, np.uint16)
+    w1q, w2q = _c(w1q, np.uint8), _c(w2q, np.uint8)
+    w1s, w2s = _c(w1s, np.float32), _c(w2s, np.float32)
+    n, D = x.shape
+    E = wg.shape[0]
+    I = w1q.shape[1] // 2
+    idx = np.empty((n, K), np.int32)
+    wts = np.empty((n, K), np.float32)
+    y = np.empty((n, D), np.float32)
+    wm = None if wmap is None else _c(wmap, np.int32)
+    lib().orc_moe_forward_fp8(x, n, wg, w1q, w1s, w2q, w2s, _opt(wm), E, K, D, I, idx, wts, y)
+    return idx, wts, y
+
+
+# ---------------------------------------------------------------- DSA
+def dsa_forward_f32(qn, qp, kc, kp, v, idx):
+    qn, qp, kc, kp, v = (_c(a, np.float32) for a in (qn, qp, kc, kp, v))
+    idx = _c(idx, np.int32)
+    Q, H, Dc = qn.shape
+    Dp = qp.shape[2]
+    S = idx.shape[1]
+    out = np.empty((Q, H, Dc), np.float32)
+    lib().orc_dsa_forward_f32(qn, qp, kc, kp, v, idx, out, Q, H, Dc, Dp, S)
+    return out
+
+
+def dsa_translate(logical, page_table, page):
+    logical = _c(logical, np.int32)
+    pt = _c(page_table, np.int32)
+    Q, S = logical.shape
+    out = np.empty((Q, S), np.int32)
+    lib().orc_dsa_translate(logical, pt, Q, S, pt.shape[1], page, out)
+    return out
+
+
+def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, Dc, page):
+    qn, qp, cache = (_c(a, np.uint16) for a in (qn, qp, cache))
+    pt = _c(page_table, np.int32)
+    logical = _c(logical, np.int32)
+    Q, H, _ = qn.shape
+    Dp = qp.shape[2]
+    S = logical.shape[1]
+    out = np.empty((Q, H, Dc), np.float32)
+    lib().orc_dsa_decode_bf16_paged(qn, qp, cache, pt, logical, out, Q, H, Dc, Dp, S,
+                                    pt.shape[1], page)
+    return out

@@ -1,0 +1,353 @@
+"""GPU parity of the MoE path, through the C ABI, against the CPU oracle.
+
+Bars: integer outputs (expert indices, permutation, fp8 codes) bit-exact;
+fp32 outputs within the reference's max-abs tolerances
+(tests/test_moe.cu:204-267, strict <); bf16 outputs within 1e-2 max-abs of
+the oracle's fp32 result; fp8 outputs within 2e-2 relative (max-abs error
+over max |ref|) of the oracle run on the same dequantised fp8 values.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cases import MOE_CASES
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    if a.dtype == np.uint8:
+        return torch.from_numpy(a).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host(t, dtype=None):
+    a = t.cpu().numpy()
+    if dtype is not None:
+        a = a.view(dtype)
+    return a
+
+
+def bf16_np(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def announce(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------ formats
+def test_quant_rows_bit_exact(amd, orc):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((37, 512)).astype(np.float32) * np.float32(3.0)
+    x[3, :128] = 0.0
+    x[5, 128:256] *= np.float32(1e-5)                     # subnormal e4m3 codes
+    x[7, 256:384] = np.float32(1.0)                       # constant block
+    xb = orc.f32_to_bf16(x)
+    xf = orc.bf16_to_f32(xb)
+    q_ref, s_ref = orc.quant_rows_1x128(xf)
+    q = torch.empty((37, 512), dtype=torch.uint8, device="cuda")
+    s = torch.empty((37, 4), dtype=torch.float32, device="cuda")
+    amd.quant_rows_fp8(dev(xb), q, s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(s), s_ref)
+    np.testing.assert_array_equal(host(q), q_ref)
+
+
+def test_quant_weight_bit_exact(amd, orc):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((256, 384)) * 0.05).astype(np.float32)
+    u = rng.uniform(0.5, 2.0, (2, 3)).astype(np.float32)
+    q_ref, s_ref = orc.quant_weight_128x128(w, u)
+    q = torch.empty((256, 384), dtype=torch.uint8, device="cuda")
+    s = torch.empty((2, 3), dtype=torch.float32, device="cuda")
+    amd.quant_weight_fp8(dev(w), dev(u), q, s)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(s), s_ref)
+    np.testing.assert_array_equal(host(q), q_ref)
+
+
+# ------------------------------------------------------------------ routing
+@pytest.mark.parametrize("name,shape,tol", MOE_CASES, ids=[c[0] for c in MOE_CASES])
+def test_gate_f32_bit_exact_on_reference_cases(amd, orc, name, shape, tol):
+    T, E, K, D, I = shape
+    announce(f"gate_f32 {name} {shape}")
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    idx_ref, wts_ref = orc.moe_route(x, wg, K)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_f32(dev(x), dev(wg), idx, wts, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6, atol=0)
+
+
+def _exact_gate_inputs(T, E, D, seed):
+    """x and Wg whose products and every partial sum are exact in fp32
+    (multiples of 2^-7 far below 2^17), so logits do not depend on the
+    summation order and ties occur often."""
+    rng = np.random.default_rng(seed)
+    x = (rng.integers(-1, 2, (T, D)) * 0.125).astype(np.float32)
+    wg = (rng.integers(-2, 3, (E, D)) * 0.0625).astype(np.float32)
+    return x, wg
+
+
+@pytest.mark.parametrize("T,E,K,D", [(64, 256, 8, 7168), (33, 64, 6, 512), (16, 16, 2, 128)])
+def test_gate_bf16_mfma_bit_exact_on_exact_logits(amd, orc, T, E, K, D):
+    announce(f"gate_bf16 exact-logit T={T} E={E} K={K} D={D}")
+    x, wg = _exact_gate_inputs(T, E, D, 11)
+    xb, wgb = orc.f32_to_bf16(x), orc.f32_to_bf16(wg)
+    idx_ref, wts_ref = orc.moe_route(x, wg, K)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16(dev(xb), dev(wgb), idx, wts, amd.moe_config(T, E, K, D, 128))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6, atol=0)
+
+
+def test_gate_bf16_mfma_random_margin_aware(amd, orc):
+    """Random N(0,1) inputs at the DSV3 gate shape.  GPU (MFMA) and CPU
+    (sequential) logits differ by rounding, so the selected set must match
+    wherever the oracle's K-th/(K+1)-th logit gap exceeds a bound on that
+    rounding; inside the bound either choice is accepted and counted."""
+    T, E, K, D = 1024, 256, 8, 7168
+    announce(f"gate_bf16 random T={T}")
+    rng = np.random.default_rng(12)
+    x = orc.bf16_to_f32(orc.f32_to_bf16(rng.standard_normal((T, D)).astype(np.float32)))
+    wg = orc.bf16_to_f32(orc.f32_to_bf16((rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)))
+    idx_ref, wts_ref, logits, _ = orc.moe_route(x, wg, K, want_probs=True)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16(dev(orc.f32_to_bf16(x)), dev(orc.f32_to_bf16(wg)), idx, wts,
+                      amd.moe_config(T, E, K, D, 128))
+    torch.cuda.synchronize()
+    gi, gw = host(idx), host(wts)
+    absdot = np.abs(x).astype(np.float64) @ np.abs(wg).astype(np.float64).T   # [T,E]
+    bound = 2 * D * 2.0 ** -24 * absdot.max(1)                                  # both sums' error
+    srt = np.sort(logits, 1)[:, ::-1]
+    margin = srt[:, K - 1] - srt[:, K]
+    same_set = np.array([set(gi[t]) == set(idx_ref[t]) for t in range(T)])
+    assert same_set[margin > 2 * bound].all()
+    same_order = (gi == idx_ref).all(1)
+    n_diff = int((~same_order).sum())
+    print(f"tokens with different slots: {n_diff} / {T}; near-ties: {(margin <= 2 * bound).sum()}")
+    assert n_diff <= max(2, T // 500)
+    ok = same_order
+    np.testing.assert_allclose(gw[ok], wts_ref[ok], rtol=1e-4, atol=1e-6)
+
+
+def test_gate_bias_and_bf16x(amd, orc):
+    T, E, K, D = 128, 8, 2, 1024
+    rng = np.random.default_rng(13)
+    x = orc.f32_to_bf16(rng.standard_normal((T, D)).astype(np.float32))
+    wg = (rng.standard_normal((E, D)) / 32).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    idx_ref, wts_ref = orc.moe_route(orc.bf16_to_f32(x), wg, K, bias=b)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16x(dev(x), dev(wg), dev(b), idx, wts, amd.moe_config(T, E, K, D, 64))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6)
+
+
+# ------------------------------------------------------------------ permutation
+@pytest.mark.parametrize("T,E,K", [(1, 4, 2), (4, 16, 2), (512, 8, 2), (4096, 256, 8), (300, 3, 5)])
+def test_permute_bit_exact(amd, orc, T, E, K):
+    announce(f"permute T={T} E={E} K={K}")
+    rng = np.random.default_rng(T + E)
+    if K <= E:
+        idx = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    else:  # K > E: the reference leaves -1 slots
+        idx = np.full((T, K), -1, np.int32)
+        idx[:, :E] = np.stack([rng.permutation(E) for _ in range(T)])
+    counts_r, offsets_r, st_r, ss_r = orc.moe_permute(idx, E)
+    P = int(offsets_r[-1])
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    st = torch.full((T * K,), -7, dtype=torch.int32, device="cuda")
+    ss = torch.full((T * K,), -7, dtype=torch.int32, device="cuda")
+    amd.moe_permute(dev(idx), amd.moe_config(T, E, K, 128, 128), counts, offsets, st, ss)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(counts), counts_r)
+    np.testing.assert_array_equal(host(offsets), offsets_r)
+    np.testing.assert_array_equal(host(st)[:P], st_r)
+    np.testing.assert_array_equal(host(ss)[:P], ss_r)
+
+
+# ------------------------------------------------------------------ stages
+def test_gather_scatter_gemm_swiglu_stages(amd, orc):
+    T, E, K, D, I = 32, 8, 2, 128, 256
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    idx_r, wts_r = orc.moe_route(x, wg, K)
+    cfg = amd.moe_config(T, E, K, D, I)
+    dx, didx, dwts = dev(x), dev(idx_r), dev(wts_r)
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    ref = np.zeros((T, D), np.float64)
+    for e in range(E):
+        gathered = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+        tmap = torch.full((T,), -1, dtype=torch.int32, device="cuda")
+        cnt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        amd.moe_gather_f32(dx, didx, dwts, e, gathered, tmap, cnt, cfg)
+        torch.cuda.synchronize()
+        c = int(cnt.item())
+        toks = [t for t in range(T) if e in idx_r[t]]
+        assert c == len(toks) and host(tmap)[:c].tolist() == toks
+        np.testing.assert_array_equal(host(gathered)[:c], x[toks])
+        if c == 0:
+            amd.moe_scatter_f32(gathered, tmap, dwts, didx, e, out, 0, cfg)
+            continue
+        # naive_gemm takes B [K,N] untransposed
+        h = torch.empty((c, 2 * I), dtype=torch.float32, device="cuda")
+        amd.naive_gemm_f32(gathered[:c].contiguous(), dev(np.ascontiguousarray(w1[e].T)), h, c, 2 * I, D)
+        a = torch.empty((c, I), dtype=torch.float32, device="cuda")
+        amd.swiglu_f32(h[:, :I].contiguous(), h[:, I:].contiguous(), a, c * I)
+        o = torch.empty((c, D), dtype=torch.float32, device="cuda")
+        amd.naive_gemm_f32(a, dev(np.ascontiguousarray(w2[e].T)), o, c, D, I)
+        amd.moe_scatter_f32(o, tmap, dwts, didx, e, out, c, cfg)
+        hh = x[toks].astype(np.float64) @ w1[e].astype(np.float64).T
+        aa = hh[:, :I] / (1 + np.exp(-hh[:, :I])) * hh[:, I:]
+        oo = aa @ w2[e].astype(np.float64).T
+        for m, t in enumerate(toks):
+            ref[t] += wts_r[t, list(idx_r[t]).index(e)] * oo[m]
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(host(out), ref, rtol=1e-4, atol=1e-6)
+
+
+# ------------------------------------------------------------------ forward f32
+@pytest.mark.parametrize("name,shape,tol", MOE_CASES, ids=[c[0] for c in MOE_CASES])
+def test_forward_f32_reference_cases(amd, orc, name, shape, tol):
+    T, E, K, D, I = shape
+    announce(f"forward_f32 {name} {shape}")
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    _, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
+    y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), y, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    err = np.abs(host(y) - y_ref).max()
+    print(f"{name}: max_err={err:.3e}")
+    assert err < tol
+    assert err < 1e-5 * max(1.0, np.abs(y_ref).max())
+
+
+def test_forward_f32_explicit_workspace_and_reuse(amd, orc):
+    T, E, K, D, I = 64, 16, 2, 512, 1024
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    _, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
+    cfg = amd.moe_config(T, E, K, D, I)
+    ws = amd.alloc_workspace(cfg, amd.AMDMOE_DTYPE_F32)
+    ys = []
+    for _ in range(3):
+        y = torch.empty((T, D), dtype=torch.float32, device="cuda")
+        amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), y, cfg, ws=ws)
+        ys.append(y)
+    torch.cuda.synchronize()
+    for y in ys:
+        np.testing.assert_array_equal(host(y), host(ys[0]))   # deterministic
+    assert np.abs(host(ys[0]) - y_ref).max() < 5e-2
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(amd.AmdMoeError):
+        amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), ys[0], cfg, ws=small)
+
+
+# ------------------------------------------------------------------ forward bf16
+def _bf16_case(amd, orc, T, E, K, D, I, bias, sample=None, seed=7):
+    import synth
+    x, wg, b, w1, w2 = synth.bf16_layer(T, E, D, I, seed=seed, bias=bias)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    amd.moe_forward_bf16(x, wg, b, w1, w2, y, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    rows = np.arange(T) if sample is None else sample
+    xs = bf16_np(x)[rows]
+    idx_r, wts_r, y_ref = orc.moe_forward_bf16(xs, host(wg), bf16_np(w1), bf16_np(w2), K,
+                                               bias=None if b is None else host(b))
+    yg = orc.bf16_to_f32(bf16_np(y)[rows])
+    err = np.abs(yg - y_ref).max()
+    print(f"bf16 T={T} E={E} D={D} I={I}: max_err={err:.3e} max|y|={np.abs(y_ref).max():.3f}")
+    return err, y_ref
+
+
+def test_forward_bf16_medium_skewed(amd, orc):
+    """BASELINE medium config in bf16, with the per-expert logit bias."""
+    announce("forward_bf16 medium")
+    err, _ = _bf16_case(amd, orc, 512, 8, 2, 1024, 2048, bias=True)
+    assert err < 1e-2
+
+
+def test_forward_bf16_mixtral_t16(amd, orc):
+    announce("forward_bf16 mixtral T=16")
+    err, _ = _bf16_case(amd, orc, 16, 8, 2, 4096, 14336, bias=False)
+    assert err < 1e-2
+
+
+def test_forward_bf16_mixtral_t4096_sampled(amd, orc):
+    """T=4096 on the GPU; the oracle checks 24 tokens (each token's output
+    depends only on its own row)."""
+    announce("forward_bf16 mixtral T=4096 sampled")
+    rows = np.random.default_rng(3).choice(4096, 24, replace=False)
+    err, _ = _bf16_case(amd, orc, 4096, 8, 2, 4096, 14336, bias=False, sample=rows)
+    assert err < 1e-2
+
+
+# ------------------------------------------------------------------ forward fp8
+@pytest.fixture(scope="module")
+def dsv3(amd):
+    import synth
+    announce("generating DSV3 fp8 weights (E=256, D=7168, I=2048)")
+    w = synth.dsv3_weights(256, 7168, 2048, seed=1234)
+    yield w
+    del w
+    torch.cuda.empty_cache()
+
+
+def _fp8_case(amd, orc, weights, T, E, K, D, I, sample=None, seed=1235):
+    import synth
+    w1q, w1s, w2q, w2s = weights
+    x, wg = synth.dsv3_inputs(T, E, D, seed=seed)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    amd.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    rows = np.arange(T) if sample is None else np.asarray(sample)
+    xs = bf16_np(x)[rows]
+    wgn = bf16_np(wg)
+    # only the experts the checked tokens use travel to the host
+    idx_s, _ = orc.moe_route(orc.bf16_to_f32(xs), orc.bf16_to_f32(wgn), K)
+    used = np.unique(idx_s[idx_s >= 0])
+    wmap = np.zeros(E, np.int32)
+    wmap[used] = np.arange(len(used), dtype=np.int32)
+    sel = torch.from_numpy(used).cuda()
+    q1 = w1q.index_select(0, sel).cpu().numpy(); s1 = w1s.index_select(0, sel).cpu().numpy()
+    q2 = w2q.index_select(0, sel).cpu().numpy(); s2 = w2s.index_select(0, sel).cpu().numpy()
+    idx_r, wts_r, y_ref = orc.moe_forward_fp8(xs, wgn, q1, s1, q2, s2, K, wmap=wmap)
+    yg = orc.bf16_to_f32(bf16_np(y)[rows])
+    rel = np.abs(yg - y_ref).max() / np.abs(y_ref).max()
+    print(f"fp8 T={T} E={E}: rel_err={rel:.3e} max|y|={np.abs(y_ref).max():.3f}")
+    return rel
+
+
+def test_forward_fp8_small_full(amd, orc):
+    import synth
+    announce("forward_fp8 small full")
+    w = synth.dsv3_weights(16, 512, 256, seed=77)
+    assert _fp8_case(amd, orc, w, 64, 16, 4, 512, 256) < 2e-2
+
+
+def test_forward_fp8_dsv3_t1(amd, orc, dsv3):
+    announce("forward_fp8 dsv3 T=1")
+    assert _fp8_case(amd, orc, dsv3, 1, 256, 8, 7168, 2048) < 2e-2
+
+
+def test_forward_fp8_dsv3_t64_full(amd, orc, dsv3):
+    announce("forward_fp8 dsv3 T=64")
+    rows = np.arange(0, 64, 4)
+    assert _fp8_case(amd, orc, dsv3, 64, 256, 8, 7168, 2048, sample=rows) < 2e-2
+
+
+def test_forward_fp8_dsv3_t4096_sampled(amd, orc, dsv3):
+    announce("forward_fp8 dsv3 T=4096 sampled")
+    rows = np.random.default_rng(4).choice(4096, 6, replace=False)
+    assert _fp8_case(amd, orc, dsv3, 4096, 256, 8, 7168, 2048, sample=rows) < 2e-2
