@@ -165,9 +165,11 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     TRY(mark(3, st));
     GemmArgs up{};
     up.a = a_x;
+    up.a_bytes = (long)T * D * es;
     up.a_row_bytes = (long)D * es;
     up.a_map = w.sorted_token;
     up.a_scale = x_scale;
+    up.a_scale_bytes = x_scale ? (long)T * (D / 128) * 4 : 0;
     up.b = w1;
     up.b_expert_bytes = 2L * I * D * es;
     up.b_row_bytes = (long)D * es;
@@ -184,8 +186,10 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     TRY(mark(4, st));
     GemmArgs dn{};
     dn.a = w.act;
+    dn.a_bytes = P * I * es;
     dn.a_row_bytes = (long)I * es;
     dn.a_scale = w.act_s;
+    dn.a_scale_bytes = w.act_s ? P * (I / 128) * 4 : 0;
     dn.b = w2;
     dn.b_expert_bytes = (long)D * I * es;
     dn.b_row_bytes = (long)I * es;

@@ -13,9 +13,11 @@ constexpr int kMTile = 128;  // rows of one grouped-GEMM M-tile
 
 struct GemmArgs {
     const uint8_t* a;        // A base
+    long a_bytes;            // bytes of the whole A array (buffer range)
     long a_row_bytes;        // bytes per A row
     const int* a_map;        // UP: sorted_token (A row of sorted position); DOWN: unused
     const float* a_scale;    // fp8: [A rows][K/128]
+    long a_scale_bytes;      // fp8: bytes of the whole a_scale array
     const uint8_t* b;        // expert weights base
     long b_expert_bytes;     // bytes per expert
     long b_row_bytes;        // bytes per weight row (K * element size)

@@ -22,11 +22,20 @@
 // one 128-wide K block, so each 16x16x128 MFMA yields a fresh partial that
 // is folded into the fp32 accumulator as acc += partial * (s_a[row]*s_b).
 //
+// Memory pipeline.  The kernel is bound by streaming expert weights from
+// HBM, so what matters is bytes in flight per CU.  Operands go global -> LDS
+// with buffer_load ... lds (no staging registers) into a 3-stage ring: while
+// a K-step is consumed, the next two are in flight (~96 KB per CU).  Buffer
+// descriptors bound every operand, so rows outside the tile (masked M rows,
+// N columns past the end) are fetched as zeros without branches.  LDS rows
+// are 128 bytes, XOR-swizzled in 16-byte chunks (chunk c of row r lives at
+// c ^ (r & 7)) so the 16 rows an MFMA fragment reads hit distinct banks.
+// Waits are explicit (vmcnt) and the barrier is a bare s_barrier, so the
+// ring is never drained mid-loop.
+//
 // Tile: 128 rows x 256 weight rows x 128 bytes of K per step; 512 threads =
 // 8 waves in a 4 (rows) x 2 (cols) grid, each wave 32 rows x 8 MFMA column
-// tiles of 16.  Operands are staged global -> registers -> LDS (double
-// buffered, one barrier per K-step); LDS rows are padded to 144 bytes so
-// the 16 rows read by a quarter-wave fall in distinct banks.
+// tiles of 16.
 //
 // Work items are laid out M-tile-major (all N-tiles of an M-tile are
 // consecutive) and dealt to XCDs in contiguous chunks (workgroup b runs on
@@ -34,28 +43,46 @@
 // the two M-tiles of an expert stay in one XCD's L2.
 #include "internal.hpp"
 
+#include <type_traits>
+
 namespace amdmoe {
 
 constexpr int kBM = 128;
-constexpr int kBRows = 256;
-constexpr int kPitch = 144;
-constexpr int kAStage = kBM * kPitch;
-constexpr int kBStage = kBRows * kPitch;
-constexpr int kStage = kAStage + kBStage + kBM * 4;
-constexpr int kEpiPitch = 132;  // floats
-constexpr int kGemmLds = (2 * kStage > kBM * kEpiPitch * 4) ? 2 * kStage : kBM * kEpiPitch * 4;
+constexpr int kNS = 3;                                 // pipeline stages
+constexpr int kATile = kBM * 128;                      // 16 KB
+constexpr int kBTile = 256 * 128;                      // 32 KB
+constexpr int kSTile = 8 * 256;                        // A-scale slots, 256 B per wave
+constexpr int kStageBytes = kATile + kBTile + kSTile;  // 51200
+constexpr int kBScaleOff = kNS * kStageBytes;          // fp8 weight scales [2][kMaxKb]
+constexpr int kMaxKb = 128;                            // K <= 16384 on the fp8 path
+constexpr int kEpiPitch = 132;                         // floats per staged output row
+constexpr int kGemmLds = kBScaleOff + 2 * kMaxKb * 4;  // 154624
+static_assert(kBM * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
+
+constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
+constexpr uint32_t kOob = 0x80000000u;   // voffset that fails the range check -> zeros
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
 template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
 template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
 
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt/lgkmcnt maxed).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <int DT, int MODE>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int ES = DtTraits<DT>::es;
-    constexpr int KE = 128 / ES;  // elements per K-step
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int kLoadsPerStage = 6 + (DT == DT_FP8 ? 1 : 0);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
 
     // ---- work item (XCD-chunked) ----
     const int W = (*g.num_tiles) * g.n_tiles_n;
@@ -67,137 +94,158 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     const int mt = w / g.n_tiles_n, nt = w - mt * g.n_tiles_n;
     const int4 tile = g.tiles[mt];
     const int e = tile.x, row0 = tile.y, rows = tile.z;
-    const int nk = g.K / KE;
+    const int nk = (int)((long)g.K * ES / 128);
     const int kb_per_row = g.K / 128;  // fp8 scale blocks along K
 
-    // ---- global source pointers of this thread ----
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    const uint8_t* asrc[2];
-    int aoff[2];
+    // ---- buffer descriptors ----
+    const uint8_t* bexp = g.b + (size_t)e * g.b_expert_bytes;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)g.a, (short)0, (int)g.a_bytes, kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)bexp, (short)0, (int)g.b_expert_bytes, kRsrcFlags);
+
+    // ---- per-lane source offsets (fixed over K; the K-step is the soffset) ----
+    const int lrow = lane >> 3;                  // row within an 8-row, 1 KB slab
+    const int lchunk = (lane & 7) ^ lrow;        // global chunk landing at lane's LDS slot
+    uint32_t voff_a[2], voff_b[4];
     for (int j = 0; j < 2; j++) {
-        int c = tid + 512 * j, r = c >> 3, ch = c & 7;
-        aoff[j] = r * kPitch + ch * 16;
-        asrc[j] = nullptr;
+        const int r = 16 * wave + 8 * j + lrow;
+        voff_a[j] = kOob;
         if (r < rows) {
-            long ar = MODE == MODE_UP ? (long)g.a_map[row0 + r] : (long)(row0 + r);
-            asrc[j] = g.a + ar * g.a_row_bytes + ch * 16;
+            const long ar = MODE == MODE_UP ? (long)g.a_map[row0 + r] : (long)(row0 + r);
+            voff_a[j] = (uint32_t)(ar * g.a_row_bytes + 16 * lchunk);
         }
     }
-    const uint8_t* bexp = g.b + (size_t)e * g.b_expert_bytes;
-    const uint8_t* bsrc[4];
-    int boff[4];
     for (int j = 0; j < 4; j++) {
-        int c = tid + 512 * j, r = c >> 3, ch = c & 7;
-        boff[j] = kAStage + r * kPitch + ch * 16;
+        const int r = 32 * wave + 8 * j + lrow;  // weight row within the 256-row tile
         long n;
         bool ok;
         if (MODE == MODE_UP) {
-            int col = nt * 128 + (r & 127);
+            const int col = nt * 128 + (r & 127);
             ok = col < g.n_out;
             n = r < 128 ? col : (long)g.n_out + col;
         } else {
             n = (long)nt * 256 + r;
             ok = n < g.n_out;
         }
-        bsrc[j] = ok ? bexp + n * g.b_row_bytes + ch * 16 : nullptr;
+        voff_b[j] = ok ? (uint32_t)(n * g.b_row_bytes + 16 * lchunk) : kOob;
     }
-    const float* assrc = nullptr;
-    if (DT == DT_FP8 && tid < kBM && tid < rows) {
-        long ar = MODE == MODE_UP ? (long)g.a_map[row0 + tid] : (long)(row0 + tid);
-        assrc = g.a_scale + ar * kb_per_row;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(DT == DT_FP8 ? (const void*)g.a_scale : (const void*)g.a), (short)0,
+        DT == DT_FP8 ? (int)g.a_scale_bytes : 0, kRsrcFlags);
+    uint32_t voff_s = kOob;
+    if (DT == DT_FP8) {
+        const int r = 16 * wave + lane;
+        if (lane < 16 && r < rows) {
+            const long ar = MODE == MODE_UP ? (long)g.a_map[row0 + r] : (long)(row0 + r);
+            voff_s = (uint32_t)(ar * kb_per_row * 4);
+        }
+        // weight scales of this work item for every K block -> LDS
+        float* sbs = (float*)(smem + kBScaleOff);
+        const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
+        for (int i = tid; i < 2 * kb_per_row; i += 512) {
+            const int which = i / kb_per_row, kb = i - which * kb_per_row;
+            int nb;
+            if (MODE == MODE_UP) nb = which == 0 ? nt : g.n_out / 128 + nt;
+            else nb = min(2 * nt + which, g.b_rows / 128 - 1);
+            sbs[which * kMaxKb + kb] = bse[(size_t)nb * kb_per_row + kb];
+        }
     }
 
-    u32x4 ra[2], rb[4];
-    float ras = 0.0f;
-    auto gload = [&](int kt) {
-        const size_t off = (size_t)kt * 128;
-        for (int j = 0; j < 2; j++) ra[j] = asrc[j] ? *(const u32x4*)(asrc[j] + off) : zero4;
-        for (int j = 0; j < 4; j++) rb[j] = bsrc[j] ? *(const u32x4*)(bsrc[j] + off) : zero4;
-        if (DT == DT_FP8) ras = assrc ? assrc[kt] : 0.0f;
-    };
-    auto sstore = [&](int st) {
-        uint8_t* base = smem + st * kStage;
-        for (int j = 0; j < 2; j++) *(u32x4*)(base + aoff[j]) = ra[j];
-        for (int j = 0; j < 4; j++) *(u32x4*)(base + boff[j]) = rb[j];
-        if (DT == DT_FP8 && tid < kBM) ((float*)(base + kAStage + kBStage))[tid] = ras;
+    auto issue = [&](int st, int kt) {
+        uint8_t* base = smem + st * kStageBytes;
+        const int soff = kt * 128;
+        for (int j = 0; j < 2; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (lds_ptr_t)(base + (16 * wave + 8 * j) * 128), 16, voff_a[j], soff, 0, 0);
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (lds_ptr_t)(base + kATile + (32 * wave + 8 * j) * 128), 16, voff_b[j], soff, 0, 0);
+        if (DT == DT_FP8)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (lds_ptr_t)(base + kATile + kBTile + wave * 256), 4, voff_s, kt * 4, 0, 0);
     };
 
     // ---- wave geometry ----
     const int wr = wave & 3, wc = wave >> 2;
     const int q = lane >> 4, r16 = lane & 15;
+    const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
     int bcol[8];
     for (int ct = 0; ct < 8; ct++)
         bcol[ct] = MODE == MODE_UP ? (ct < 4 ? 64 * wc + 16 * ct : 128 + 64 * wc + 16 * (ct - 4))
                                    : 128 * wc + 16 * ct;
     const bool rt_on[2] = {32 * wr < rows, 32 * wr + 16 < rows};
-
-    // fp8 weight-scale rows of this wave
-    const float* bs0 = nullptr;
-    const float* bs1 = nullptr;
-    if (DT == DT_FP8) {
-        const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
-        if (MODE == MODE_UP) {
-            bs0 = bse + (size_t)nt * kb_per_row;                       // gate block
-            bs1 = bse + (size_t)(g.n_out / 128 + nt) * kb_per_row;     // up block
-        } else {
-            int nb = 2 * nt + wc;
-            if (nb >= g.b_rows / 128) nb = g.b_rows / 128 - 1;         // masked columns
-            bs0 = bs1 = bse + (size_t)nb * kb_per_row;
-        }
-    }
+    const int nrt = (int)rt_on[0] + (int)rt_on[1];  // live row tiles of this wave (uniform)
 
     f32x4 acc[2][8];
     for (int i = 0; i < 2; i++)
         for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
+    __syncthreads();  // weight scales in LDS; every regular load has completed
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
     for (int kt = 0; kt < nk; kt++) {
-        if (kt + 1 < nk) gload(kt + 1);
-        const uint8_t* base = smem + (kt & 1) * kStage;
-        u32x4 alo[2], ahi[2];
-        float sa[2][4];
-        for (int rt = 0; rt < 2; rt++) {
-            if (!rt_on[rt]) continue;
-            const uint8_t* p = base + (32 * wr + 16 * rt + r16) * kPitch + 16 * q;
-            alo[rt] = *(const u32x4*)p;
-            ahi[rt] = *(const u32x4*)(p + 64);
-            if (DT == DT_FP8) {
-                f32x4 s4 = *(const f32x4*)(base + kAStage + kBStage + 4 * (32 * wr + 16 * rt + 4 * q));
-                for (int i = 0; i < 4; i++) sa[rt][i] = s4[i];
-            }
-        }
+        if (kt + 1 < nk) wait_vmcnt<kLoadsPerStage>();
+        else wait_vmcnt<0>();
+        // bare barrier (no fence, so the ring is not drained); the empty asm
+        // keeps the compiler from moving LDS accesses across it
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + 2 < nk) issue((kt + 2) % kNS, kt + 2);
+
+        const uint8_t* base = smem + (kt % kNS) * kStageBytes;
         float sb0 = 0.f, sb1 = 0.f;
-        if (DT == DT_FP8) { sb0 = bs0[kt]; sb1 = bs1[kt]; }
-        for (int ct = 0; ct < 8; ct++) {
-            const uint8_t* p = base + kAStage + (bcol[ct] + r16) * kPitch + 16 * q;
-            u32x4 blo = *(const u32x4*)p, bhi = *(const u32x4*)(p + 64);
-            for (int rt = 0; rt < 2; rt++) {
-                if (!rt_on[rt]) continue;
-                if (DT == DT_F32) {
-                    for (int j = 0; j < 4; j++)
-                        acc[rt][ct] = mfma_f32(__uint_as_float(alo[rt][j]), __uint_as_float(blo[j]), acc[rt][ct]);
-                    for (int j = 0; j < 4; j++)
-                        acc[rt][ct] = mfma_f32(__uint_as_float(ahi[rt][j]), __uint_as_float(bhi[j]), acc[rt][ct]);
-                } else if (DT == DT_BF16) {
-                    acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
-                    acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
-                } else {
-                    i32x8 av, bv;
-                    for (int j = 0; j < 4; j++) {
-                        av[j] = (int)alo[rt][j]; av[4 + j] = (int)ahi[rt][j];
-                        bv[j] = (int)blo[j];     bv[4 + j] = (int)bhi[j];
-                    }
-                    f32x4 pr = mfma_fp8(av, bv, (f32x4){0.f, 0.f, 0.f, 0.f});
-                    const float sb = (MODE == MODE_UP && ct >= 4) ? sb1 : sb0;
-                    for (int i = 0; i < 4; i++) acc[rt][ct][i] += pr[i] * (sa[rt][i] * sb);
+        if (DT == DT_FP8) {
+            const float* sbs = (const float*)(smem + kBScaleOff);
+            if (MODE == MODE_UP) { sb0 = sbs[kt]; sb1 = sbs[kMaxKb + kt]; }
+            else { sb0 = sb1 = sbs[wc * kMaxKb + kt]; }
+        }
+        // one K-step for NRT (1 or 2) live row tiles of 16, straight-line so
+        // the scheduler can overlap MFMAs with fragment loads and scaling
+        auto step = [&](auto nrt_tag) {
+            constexpr int NRT = decltype(nrt_tag)::value;
+            u32x4 alo[NRT], ahi[NRT];
+            float sa[NRT][4];
+            for (int rt = 0; rt < NRT; rt++) {
+                const uint8_t* p = base + (32 * wr + 16 * rt + r16) * 128;
+                alo[rt] = *(const u32x4*)(p + off_lo);
+                ahi[rt] = *(const u32x4*)(p + off_hi);
+                if (DT == DT_FP8) {
+                    const int r = 32 * wr + 16 * rt + 4 * q;  // 4 rows inside one 16-row slot
+                    const f32x4 s4 = *(const f32x4*)(base + kATile + kBTile + (r >> 4) * 256 + (r & 15) * 4);
+                    for (int i = 0; i < 4; i++) sa[rt][i] = s4[i];
                 }
             }
-        }
-        if (kt + 1 < nk) sstore((kt + 1) & 1);
-        __syncthreads();
+            for (int ct = 0; ct < 8; ct++) {
+                const uint8_t* p = base + kATile + (bcol[ct] + r16) * 128;
+                const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
+                for (int rt = 0; rt < NRT; rt++) {
+                    if (DT == DT_F32) {
+                        for (int j = 0; j < 4; j++)
+                            acc[rt][ct] = mfma_f32(__uint_as_float(alo[rt][j]), __uint_as_float(blo[j]), acc[rt][ct]);
+                        for (int j = 0; j < 4; j++)
+                            acc[rt][ct] = mfma_f32(__uint_as_float(ahi[rt][j]), __uint_as_float(bhi[j]), acc[rt][ct]);
+                    } else if (DT == DT_BF16) {
+                        acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
+                        acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
+                    } else {
+                        i32x8 av, bv;
+                        for (int j = 0; j < 4; j++) {
+                            av[j] = (int)alo[rt][j]; av[4 + j] = (int)ahi[rt][j];
+                            bv[j] = (int)blo[j];     bv[4 + j] = (int)bhi[j];
+                        }
+                        const f32x4 pr = mfma_fp8(av, bv, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        const float sb = (MODE == MODE_UP && ct >= 4) ? sb1 : sb0;
+                        for (int i = 0; i < 4; i++) acc[rt][ct][i] += pr[i] * (sa[rt][i] * sb);
+                    }
+                }
+            }
+        };
+        if (nrt == 2) step(std::integral_constant<int, 2>{});
+        else if (nrt == 1) step(std::integral_constant<int, 1>{});
     }
+    __syncthreads();  // every wave is done with the ring before it is reused
 
     // ---- epilogues (LDS staging for coalesced 16-byte stores) ----
     float* T = (float*)smem;
@@ -207,8 +255,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             if (!rt_on[rt]) continue;
             for (int j = 0; j < 4; j++)
                 for (int i = 0; i < 4; i++) {
-                    float gv = acc[rt][j][i], uv = acc[rt][j + 4][i];
-                    float silu = gv / (1.0f + expf(-gv));
+                    const float gv = acc[rt][j][i], uv = acc[rt][j + 4][i];
+                    const float silu = gv / (1.0f + expf(-gv));
                     T[(32 * wr + 16 * rt + 4 * q + i) * kEpiPitch + 64 * wc + 16 * j + r16] = silu * uv;
                 }
         }
@@ -312,6 +360,12 @@ static int launch_one(const GemmArgs& g, long max_tiles, hipStream_t st) {
 }
 
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st) {
+    // buffer descriptors address at most 4 GiB - 1 bytes per operand
+    const long lim = 0xFFFFFFF0L;
+    AMDMOE_CHECK_ARG(g.a_bytes <= lim && g.b_expert_bytes <= lim && g.a_scale_bytes <= lim,
+                     "grouped gemm: an operand exceeds 4 GiB (A %ld, expert %ld bytes)", g.a_bytes,
+                     g.b_expert_bytes);
+    AMDMOE_CHECK_ARG(dt != DT_FP8 || g.K / 128 <= kMaxKb, "grouped gemm: K=%d too large for fp8", g.K);
     if (dt == DT_F32) return mode == MODE_UP ? launch_one<DT_F32, MODE_UP>(g, max_tiles, st)
                                              : launch_one<DT_F32, MODE_DOWN>(g, max_tiles, st);
     if (dt == DT_BF16) return mode == MODE_UP ? launch_one<DT_BF16, MODE_UP>(g, max_tiles, st)
