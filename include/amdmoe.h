@@ -186,7 +186,9 @@ int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* 
  * [Q, pages_per_seq]; logical_indices int32 [Q,S] are positions in the
  * query's sequence, physical row = page_table[q][i/page]*page + i%page.
  * q_nope bf16 [Q,H,Dc], q_pe bf16 [Q,H,Dp]; out bf16 [Q,H,Dc].
- * Requires Dc == 512, Dp == 64, H a multiple of 16. */
+ * cfg->total_kv_tokens is the number of rows of `cache` (it bounds every
+ * access); cfg->page_size is the page length.
+ * Requires Dc == 512, Dp == 64, H a multiple of 32, 1 <= S <= 4096. */
 int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const uint16_t* cache, const int* page_table,
                                  const int* logical_indices, uint16_t* output,

@@ -410,8 +410,9 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const DsaConfig* cfg, int pages_per_seq, void* stream) {
     AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
     const DsaConfig& c = *cfg;
-    return launch_dsa_bf16_paged(q_nope, q_pe, cache, page_table, logical_indices, output,
-                                 c.num_queries, c.num_heads, c.head_dim_compressed,
+    return launch_dsa_bf16_paged(q_nope, q_pe, cache, c.total_kv_tokens, page_table,
+                                 logical_indices, output, c.num_queries, c.num_heads,
+                                 c.head_dim_compressed,
                                  c.head_dim_positional, c.num_selected_kv, c.page_size,
                                  pages_per_seq, (hipStream_t)stream);
 }

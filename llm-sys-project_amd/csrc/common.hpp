@@ -116,6 +116,34 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// ------------------------------------------------------------------ LDS DMA
+// Direct global->LDS loads (buffer_load ... lds): lane l of a wave writes its
+// `size` bytes at M0 + l*size, where M0 is the (wave-uniform) LDS pointer.
+// A voffset past the descriptor's range reads as zeros.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
+constexpr uint32_t kOob = 0x80000000u;   // voffset that fails the range check
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, kRsrcFlags);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt/lgkmcnt maxed).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would
+// wait for every outstanding load, draining a DMA ring); the empty asm
+// statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ host
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline long ceil_div(long a, long b) { return (a + b - 1) / b; }

@@ -23,9 +23,8 @@
 //     O^T += V^T . P^T   (bf16 MFMA; P^T is already in the B-operand layout
 //                         because S^T's output layout gives each lane the
 //                         8 tokens {4g..4g+3, 16+4g..16+4g+3} of its head)
-//   V^T fragments come from a 4-token-interleaved copy of the K_c part, so
-//   each MFMA operand is two 8-byte LDS reads.  The two token halves merge
-//   through LDS at the end.
+//   V^T fragments are read from the same row-major tile with the gfx950
+//   transposing LDS read.  The two token halves merge through LDS at the end.
 #include "internal.hpp"
 
 #include <float.h>
@@ -90,39 +89,65 @@ int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const floa
 }
 
 // ---------------------------------------------------------------- bf16 paged
+// Geometry: Dc = 512, Dp = 64, one latent row = 576 bf16 = 1152 bytes = 72
+// chunks of 16 bytes.  A stage holds 32 token rows densely (36 KB), chunk j
+// of token r stored at chunk position j ^ (r & 7) (conflict-free 16-row
+// reads).  Workgroup = one query x 32 heads, 4 waves: wave (hg, th) owns
+// heads [16hg, 16hg+16) of the group and tokens [16th, 16th+16) of every
+// stage.  The stages are filled by direct global->LDS loads (36 per stage,
+// 9 per wave) through a 3-stage ring; each lane loads the chunk of the
+// token whose physical row the page table gives.
+//   S^T (16 tok x 16 heads) = K . Q^T : 18 MFMA 16x16x32, A = K rows (LDS),
+//                                       B = q (registers, loaded once)
+//   online softmax per head in the exp2 domain; the running max is raised
+//   only when a tile's max exceeds it by more than 8 (p <= 256 in bf16),
+//   so the O rescale is rare
+//   O^T (512 d x 16 heads) += V^T . P^T : 32 MFMA 16x16x16; P^T comes
+//   straight from S^T's output layout (lane = head, 4 tokens), V^T
+//   fragments from the row-major K_c tile with ds_read_b64_tr_b16.
 constexpr int kDc = 512, kDp = 64, kDt = 576;
-constexpr int kRowBytes = kDt * 2;            // 1152
-constexpr int kKPitch = kRowBytes + 16;       // 1168: conflict-free 16-row b128 reads
+constexpr int kRowBytes = kDt * 2;               // 1152
+constexpr int kRowChunks = kRowBytes / 16;       // 72
 constexpr int kTileTok = 32;
-constexpr int kKBuf = kTileTok * kKPitch;     // 37376
-constexpr int kVBuf = (kTileTok / 4) * kDc * 8;  // 32768: [quad][d][4 tokens] bf16
-constexpr int kBuf = kKBuf + kVBuf;           // 70144
+constexpr int kStageB = kTileTok * kRowBytes;    // 36864
+constexpr int kDsaNS = 3;
 constexpr int kMaxS = 4096;
-constexpr int kDsaLds = 2 * kBuf + kMaxS * 4;  // 156672
+constexpr int kRowsOff = kDsaNS * kStageB;       // 110592
+constexpr int kDsaLds = kRowsOff + kMaxS * 4;    // 126976
+constexpr int kLoadsPerWave = kStageB / 1024 / 4;  // 9
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
-    const uint16_t* __restrict__ cache, const int* __restrict__ page_table,
-    const int* __restrict__ logical, uint16_t* __restrict__ out, int H, int S, int page,
-    int pages_per_seq, float scale) {
+    const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
+    const int* __restrict__ logical, uint16_t* __restrict__ out, int Q, int H, int S, int page,
+    int pages_per_seq, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    int* s_rows = (int*)(smem + 2 * kBuf);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int* s_rows = (int*)(smem + kRowsOff);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // query-major block order, 4 head groups of one query adjacent: with
+    // block b on XCD b % 8, remap so a query's 4 blocks share an XCD (its
+    // latent rows are then read from HBM once and served to all 4 from L2)
+    const int nblk = gridDim.x, per = nblk / 8;
+    const int lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
     const int hgroups = H / 32;
-    const int qi = blockIdx.x / hgroups;
-    const int h0 = (blockIdx.x % hgroups) * 32;
+    const int qi = lin / hgroups;
+    if (qi >= Q) return;  // padding block of the XCD remap
+    const int h0 = (lin % hgroups) * 32;
     const int hg = wave & 1, th = wave >> 1;
     const int g = lane >> 4, c16 = lane & 15;
     const int my_head = h0 + 16 * hg + c16;
 
-    // page-table translation of all of this query's indices
+    // page-table translation of this query's indices: physical row, or -1
     for (int s = tid; s < S; s += 256) {
-        int i = logical[(size_t)qi * S + s];
+        const int i = logical[(size_t)qi * S + s];
         s_rows[s] = page_table[(size_t)qi * pages_per_seq + i / page] * page + i % page;
     }
 
-    // q of my head as MFMA B fragments: 18 K-steps of 32 dims, lane group g
-    // holds dims 32ks + 8g .. +7.
+    // q of my head as B fragments: 18 K-steps of 32 dims, group g holds 8
     u32x4 qf[18];
     {
         const uint16_t* qnr = qn + ((size_t)qi * H + my_head) * kDc;
@@ -130,120 +155,98 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
         for (int ks = 0; ks < 16; ks++) qf[ks] = *(const u32x4*)(qnr + 32 * ks + 8 * g);
         for (int ks = 0; ks < 2; ks++) qf[16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
     }
-    __syncthreads();
+    __syncthreads();  // s_rows visible; regular loads complete
 
-    // load assignment per 64-token step: Kc units (buffer b, quad, dchunk)
-    // = 2*8*64 = 1024 -> 4 per thread (4 tokens x 16 B each); Kp chunks
-    // 2*32*8 = 512 -> 2 per thread.
-    const uint8_t* cbase = (const uint8_t*)cache;
-    u32x4 rk[4][4], rp[2];
-    auto tok_row = [&](int s) -> long { return s < S ? (long)s_rows[s] : -1L; };
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    auto gload = [&](int step) {
-        const int tbase = step * 64;
-        for (int j = 0; j < 4; j++) {
-            int u = tid + 256 * j;
-            int b = u >> 9, quad = (u >> 6) & 7, dch = u & 63;
-            for (int t4 = 0; t4 < 4; t4++) {
-                long r = tok_row(tbase + 32 * b + 4 * quad + t4);
-                rk[j][t4] = r >= 0 ? *(const u32x4*)(cbase + r * kRowBytes + dch * 16) : zero4;
-            }
-        }
-        for (int j = 0; j < 2; j++) {
-            int u = tid + 256 * j;
-            int b = u >> 8, t = (u >> 3) & 31, dch = u & 7;
-            long r = tok_row(tbase + 32 * b + t);
-            rp[j] = r >= 0 ? *(const u32x4*)(cbase + r * kRowBytes + 1024 + dch * 16) : zero4;
-        }
-    };
-    auto sstore = [&]() {
-        for (int j = 0; j < 4; j++) {
-            int u = tid + 256 * j;
-            int b = u >> 9, quad = (u >> 6) & 7, dch = u & 63;
-            uint8_t* kb = smem + b * kBuf;
-            for (int t4 = 0; t4 < 4; t4++)
-                *(u32x4*)(kb + (4 * quad + t4) * kKPitch + dch * 16) = rk[j][t4];
-            // interleave: for each of the 8 dims, the 4 tokens' values
-            uint8_t* vb = kb + kKBuf + ((size_t)quad * kDc + dch * 8) * 8;
-            for (int dd = 0; dd < 8; dd++) {
-                const int w = dd >> 1, sh = (dd & 1) * 16;
-                uint32_t v0 = (rk[j][0][w] >> sh) & 0xffffu, v1 = (rk[j][1][w] >> sh) & 0xffffu;
-                uint32_t v2 = (rk[j][2][w] >> sh) & 0xffffu, v3 = (rk[j][3][w] >> sh) & 0xffffu;
-                u32x2 pk = {v0 | (v1 << 16), v2 | (v3 << 16)};
-                *(u32x2*)(vb + dd * 8) = pk;
-            }
-        }
-        for (int j = 0; j < 2; j++) {
-            int u = tid + 256 * j;
-            int b = u >> 8, t = (u >> 3) & 31, dch = u & 7;
-            *(u32x4*)(smem + b * kBuf + t * kKPitch + 1024 + dch * 16) = rp[j];
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
+    auto issue = [&](int st, int tile) {
+        uint8_t* base = smem + st * kStageB;
+        for (int n = 0; n < kLoadsPerWave; n++) {
+            const int c = 64 * (kLoadsPerWave * wave + n) + lane;  // chunk position in the stage
+            const int r = c / kRowChunks, jp = c - r * kRowChunks;
+            const int tok = tile * kTileTok + r;
+            const int j = jp ^ (r & 7);
+            const uint32_t vo = tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * j) : kOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rc, (lds_ptr_t)(base + 1024 * (kLoadsPerWave * wave + n)), 16, vo, 0, 0, 0);
         }
     };
 
     f32x4 o[32];
+#pragma unroll
     for (int i = 0; i < 32; i++) o[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
-    const int nsteps = (S + 63) / 64;
-    const float kLog2e = 1.4426950408889634f;
+    const int ntiles = (S + kTileTok - 1) / kTileTok;
 
-    gload(0);
-    for (int step = 0; step < nsteps; step++) {
-        sstore();
-        __syncthreads();
-        if (step + 1 < nsteps) gload(step + 1);
-        const uint8_t* kb = smem + th * kBuf;
-        const int tok0 = step * 64 + 32 * th;
-        // S^T tiles: tokens 0-15 and 16-31 of this half
-        f32x4 sacc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
-        for (int ks = 0; ks < 18; ks++) {
-            for (int mt = 0; mt < 2; mt++) {
-                u32x4 a = *(const u32x4*)(kb + (16 * mt + c16) * kKPitch + (32 * ks + 8 * g) * 2);
-                sacc[mt] = mfma_bf16(a, qf[ks], sacc[mt]);
-            }
+    // per-lane LDS addresses (bytes within a stage)
+    const int r_s = 16 * th + c16;  // token row read for S^T (A operand)
+    // V^T transposed read: lane (g, s) supplies token 4g + (s>>2) of this
+    // half, dims d0 + 4(s&3) .. +3
+    const int r_v = 16 * th + 4 * g + (c16 >> 2);
+    const int vsub = 4 * (c16 & 3);
+
+    issue(0, 0);
+    if (ntiles > 1) issue(1, 1);
+    for (int t = 0; t < ntiles; t++) {
+        if (t + 1 < ntiles) wait_vmcnt<kLoadsPerWave>();
+        else wait_vmcnt<0>();
+        bare_barrier();
+        if (t + 2 < ntiles) issue((t + 2) % kDsaNS, t + 2);
+        const uint8_t* kb = smem + (t % kDsaNS) * kStageB;
+
+        // S^T: two independent accumulation chains over the 18 K-steps
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb2 = {0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < 18; ks += 2) {
+            const u32x4 a0 = *(const u32x4*)(kb + r_s * kRowBytes + 16 * ((4 * ks + g) ^ (r_s & 7)));
+            const u32x4 a1 = *(const u32x4*)(kb + r_s * kRowBytes + 16 * ((4 * ks + 4 + g) ^ (r_s & 7)));
+            sa = mfma_bf16(a0, qf[ks], sa);
+            sb2 = mfma_bf16(a1, qf[ks + 1], sb2);
         }
-        // lane: head c16, tokens 16*mt + 4g + i
-        float sv[8];
+        // lane: head c16, tokens 16th + 4g + i of this tile
+        float sv[4];
         float tmax = -INFINITY;
-        for (int mt = 0; mt < 2; mt++)
-            for (int i = 0; i < 4; i++) {
-                int tk = tok0 + 16 * mt + 4 * g + i;
-                float s = tk < S ? sacc[mt][i] * scale : -INFINITY;
-                sv[4 * mt + i] = s;
-                tmax = fmaxf(tmax, s);
-            }
+        for (int i = 0; i < 4; i++) {
+            const int tk = t * kTileTok + 16 * th + 4 * g + i;
+            sv[i] = tk < S ? (sa[i] + sb2[i]) * scale_log2 : -INFINITY;
+            tmax = fmaxf(tmax, sv[i]);
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float corr = m_new == -INFINITY ? 1.0f : exp2f((m_run - m_new) * kLog2e);
-        float psum = 0.0f;
-        float pv[8];
-        for (int j = 0; j < 8; j++) {
-            pv[j] = m_new == -INFINITY ? 0.0f : exp2f((sv[j] - m_new) * kLog2e);
-            psum += pv[j];
+        const bool raise = tmax > m_run + 8.0f;
+        if (__ballot(raise)) {  // rare after the first tile: rescale O
+            const float m_new = raise ? tmax : m_run;
+            const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - m_new);
+            l_run *= corr;
+#pragma unroll
+            for (int i = 0; i < 32; i++) o[i] *= corr;
+            m_run = m_new;
+        }
+        float pv[4], psum = 0.0f;
+        for (int i = 0; i < 4; i++) {
+            pv[i] = sv[i] == -INFINITY ? 0.0f : exp2f(sv[i] - m_run);
+            psum += pv[i];
         }
         psum += __shfl_xor(psum, 16, 64);
         psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-        u32x4 pb = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
-                    pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])};
-        const uint8_t* vb = kb + kKBuf;
+        l_run += psum;
+        const u32x2 pb2 = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+        const s16x4 pb = __builtin_bit_cast(s16x4, pb2);
+#pragma unroll
         for (int mt = 0; mt < 32; mt++) {
-            o[mt] *= corr;
-            const int d = 16 * mt + c16;
-            u32x2 lo = *(const u32x2*)(vb + ((size_t)g * kDc + d) * 8);
-            u32x2 hi = *(const u32x2*)(vb + ((size_t)(4 + g) * kDc + d) * 8);
-            u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-            o[mt] = mfma_bf16(a, pb, o[mt]);
+            const int dd = 16 * mt + vsub;
+            const uint8_t* va = kb + r_v * kRowBytes + 16 * ((dd >> 3) ^ (r_v & 7)) + 8 * ((dd >> 2) & 1);
+            const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(va));
+            o[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, o[mt], 0, 0, 0);
         }
-        __syncthreads();
     }
+    __syncthreads();  // ring no longer read; reuse it for the merge
 
     // merge the two token halves: wave (hg, 1) hands (m, l, O) to wave (hg, 0)
-    float* xch = (float*)smem;  // [hg][32 mt][4][64 lanes] + m/l
-    float* xml = (float*)(smem + 2 * 32 * 4 * 64 * 4);
+    float* xch = (float*)smem;                              // [hg][32 mt][4][64 lanes]
+    float* xml = (float*)(smem + 2 * 32 * 4 * 64 * 4);      // [hg][2][64]
     if (th == 1) {
+#pragma unroll
         for (int mt = 0; mt < 32; mt++)
+#pragma unroll
             for (int i = 0; i < 4; i++) xch[((hg * 32 + mt) * 4 + i) * 64 + lane] = o[mt][i];
         xml[(hg * 2 + 0) * 64 + lane] = m_run;
         xml[(hg * 2 + 1) * 64 + lane] = l_run;
@@ -252,28 +255,33 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     if (th == 0) {
         const float m1 = xml[(hg * 2 + 0) * 64 + lane], l1 = xml[(hg * 2 + 1) * 64 + lane];
         const float m = fmaxf(m_run, m1);
-        const float c0 = m_run == -INFINITY ? 0.0f : exp2f((m_run - m) * kLog2e);
-        const float c1 = m1 == -INFINITY ? 0.0f : exp2f((m1 - m) * kLog2e);
+        const float c0 = m_run == -INFINITY ? 0.0f : exp2f(m_run - m);
+        const float c1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - m);
         const float l = l_run * c0 + l1 * c1;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         uint16_t* orow = out + ((size_t)qi * H + my_head) * kDc;
+#pragma unroll
         for (int mt = 0; mt < 32; mt++) {
             float r[4];
+#pragma unroll
             for (int i = 0; i < 4; i++)
                 r[i] = (o[mt][i] * c0 + xch[((hg * 32 + mt) * 4 + i) * 64 + lane] * c1) * inv;
-            u32x2 pk = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
+            const u32x2 pk = {pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
             *(u32x2*)(orow + 16 * mt + 4 * g) = pk;
         }
     }
 }
 
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
-                          const int* page_table, const int* logical, uint16_t* out, int Q, int H,
-                          int Dc, int Dp, int S, int page, int pages_per_seq, hipStream_t st) {
+                          long cache_tokens, const int* page_table, const int* logical,
+                          uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
+                          int pages_per_seq, hipStream_t st) {
     AMDMOE_CHECK_ARG(Dc == kDc && Dp == kDp, "dsa_decode_bf16_paged: needs Dc=512, Dp=64 (got %d, %d)", Dc, Dp);
     AMDMOE_CHECK_ARG(H % 32 == 0 && H > 0, "dsa_decode_bf16_paged: H=%d not a multiple of 32", H);
     AMDMOE_CHECK_ARG(S >= 1 && S <= kMaxS, "dsa_decode_bf16_paged: S=%d outside [1, %d]", S, kMaxS);
     AMDMOE_CHECK_ARG(page >= 1 && pages_per_seq >= 1, "dsa_decode_bf16_paged: bad paging");
+    AMDMOE_CHECK_ARG(cache_tokens >= 1 && cache_tokens * kRowBytes <= 0xFFFFFFF0L,
+                     "dsa_decode_bf16_paged: cache of %ld tokens outside (0, 4 GiB)", cache_tokens);
     if (Q == 0) return AMDMOE_OK;
     static bool attr_set = false;
     if (!attr_set) {
@@ -281,9 +289,14 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kDsaLds));
         attr_set = true;
     }
-    const float scale = 1.0f / sqrtf((float)(Dc + Dp));
-    hipLaunchKernelGGL(dsa_bf16_paged_kernel, dim3(Q * (H / 32)), dim3(256), kDsaLds, st, qn, qp,
-                       cache, page_table, logical, out, H, S, page, pages_per_seq, scale);
+    // blocks = Q * H/32, padded to a multiple of 8 for the XCD remap; the
+    // padding blocks map past the last query and exit
+    const int nblk = Q * (H / 32);
+    const int grid = (nblk + 7) / 8 * 8;
+    const float scale_log2 = 1.0f / sqrtf((float)(Dc + Dp)) * 1.4426950408889634f;
+    hipLaunchKernelGGL(dsa_bf16_paged_kernel, dim3(grid), dim3(256), kDsaLds, st, qn, qp, cache,
+                       cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,
+                       pages_per_seq, scale_log2);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }

@@ -74,7 +74,8 @@ int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const floa
                    const float* v, const int* idx, float* out, int Q, int H, int Dc, int Dp, int S,
                    int N, hipStream_t st);
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
-                          const int* page_table, const int* logical, uint16_t* out, int Q, int H,
-                          int Dc, int Dp, int S, int page, int pages_per_seq, hipStream_t st);
+                          long cache_tokens, const int* page_table, const int* logical,
+                          uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
+                          int pages_per_seq, hipStream_t st);
 
 }  // namespace amdmoe

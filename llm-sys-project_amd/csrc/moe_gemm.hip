@@ -34,8 +34,11 @@
 // ring is never drained mid-loop.
 //
 // Tile: 128 rows x 256 weight rows x 128 bytes of K per step; 512 threads =
-// 8 waves in a 4 (rows) x 2 (cols) grid, each wave 32 rows x 8 MFMA column
-// tiles of 16.
+// 8 waves in a 2 (rows) x 4 (cols) grid, each wave 64 rows (4 MFMA row tiles
+// of 16) x 64 weight rows (4 column tiles): the square wave tile minimises
+// LDS fragment traffic, (64 + 64) x 128 bytes per wave per K-step.  In the
+// up-projection a wave's 64 weight rows are 32 gate rows and the 32 matching
+// up rows.
 //
 // Work items are laid out M-tile-major (all N-tiles of an M-tile are
 // consecutive) and dealt to XCDs in contiguous chunks (workgroup b runs on
@@ -59,22 +62,10 @@ constexpr int kEpiPitch = 132;                         // floats per staged outp
 constexpr int kGemmLds = kBScaleOff + 2 * kMaxKb * 4;  // 154624
 static_assert(kBM * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
 
-constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
-constexpr uint32_t kOob = 0x80000000u;   // voffset that fails the range check -> zeros
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
 template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
 template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt/lgkmcnt maxed).
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int DT, int MODE>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
@@ -167,19 +158,19 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     };
 
     // ---- wave geometry ----
-    const int wr = wave & 3, wc = wave >> 2;
+    const int wr = wave & 1, wc = wave >> 1;
     const int q = lane >> 4, r16 = lane & 15;
     const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
-    int bcol[8];
-    for (int ct = 0; ct < 8; ct++)
-        bcol[ct] = MODE == MODE_UP ? (ct < 4 ? 64 * wc + 16 * ct : 128 + 64 * wc + 16 * (ct - 4))
-                                   : 128 * wc + 16 * ct;
-    const bool rt_on[2] = {32 * wr < rows, 32 * wr + 16 < rows};
-    const int nrt = (int)rt_on[0] + (int)rt_on[1];  // live row tiles of this wave (uniform)
+    int bcol[4];
+    for (int ct = 0; ct < 4; ct++)
+        bcol[ct] = MODE == MODE_UP ? (ct < 2 ? 32 * wc + 16 * ct : 128 + 32 * wc + 16 * (ct - 2))
+                                   : 64 * wc + 16 * ct;
+    int nrt = (rows - 64 * wr + 15) / 16;  // live row tiles of this wave (uniform)
+    nrt = nrt < 0 ? 0 : (nrt > 4 ? 4 : nrt);
 
-    f32x4 acc[2][8];
-    for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 8; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[4][4];
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     __syncthreads();  // weight scales in LDS; every regular load has completed
     issue(0, 0);
@@ -187,11 +178,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     for (int kt = 0; kt < nk; kt++) {
         if (kt + 1 < nk) wait_vmcnt<kLoadsPerStage>();
         else wait_vmcnt<0>();
-        // bare barrier (no fence, so the ring is not drained); the empty asm
-        // keeps the compiler from moving LDS accesses across it
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
+        bare_barrier();
         if (kt + 2 < nk) issue((kt + 2) % kNS, kt + 2);
 
         const uint8_t* base = smem + (kt % kNS) * kStageBytes;
@@ -199,25 +186,25 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         if (DT == DT_FP8) {
             const float* sbs = (const float*)(smem + kBScaleOff);
             if (MODE == MODE_UP) { sb0 = sbs[kt]; sb1 = sbs[kMaxKb + kt]; }
-            else { sb0 = sb1 = sbs[wc * kMaxKb + kt]; }
+            else { sb0 = sb1 = sbs[(wc >> 1) * kMaxKb + kt]; }
         }
-        // one K-step for NRT (1 or 2) live row tiles of 16, straight-line so
+        // one K-step for NRT (1..4) live row tiles of 16, straight-line so
         // the scheduler can overlap MFMAs with fragment loads and scaling
         auto step = [&](auto nrt_tag) {
             constexpr int NRT = decltype(nrt_tag)::value;
             u32x4 alo[NRT], ahi[NRT];
             float sa[NRT][4];
             for (int rt = 0; rt < NRT; rt++) {
-                const uint8_t* p = base + (32 * wr + 16 * rt + r16) * 128;
+                const uint8_t* p = base + (64 * wr + 16 * rt + r16) * 128;
                 alo[rt] = *(const u32x4*)(p + off_lo);
                 ahi[rt] = *(const u32x4*)(p + off_hi);
                 if (DT == DT_FP8) {
-                    const int r = 32 * wr + 16 * rt + 4 * q;  // 4 rows inside one 16-row slot
+                    const int r = 64 * wr + 16 * rt + 4 * q;  // 4 rows inside one 16-row slot
                     const f32x4 s4 = *(const f32x4*)(base + kATile + kBTile + (r >> 4) * 256 + (r & 15) * 4);
                     for (int i = 0; i < 4; i++) sa[rt][i] = s4[i];
                 }
             }
-            for (int ct = 0; ct < 8; ct++) {
+            for (int ct = 0; ct < 4; ct++) {
                 const uint8_t* p = base + kATile + (bcol[ct] + r16) * 128;
                 const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
                 for (int rt = 0; rt < NRT; rt++) {
@@ -236,13 +223,15 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                             bv[j] = (int)blo[j];     bv[4 + j] = (int)bhi[j];
                         }
                         const f32x4 pr = mfma_fp8(av, bv, (f32x4){0.f, 0.f, 0.f, 0.f});
-                        const float sb = (MODE == MODE_UP && ct >= 4) ? sb1 : sb0;
+                        const float sb = (MODE == MODE_UP && ct >= 2) ? sb1 : sb0;
                         for (int i = 0; i < 4; i++) acc[rt][ct][i] += pr[i] * (sa[rt][i] * sb);
                     }
                 }
             }
         };
-        if (nrt == 2) step(std::integral_constant<int, 2>{});
+        if (nrt == 4) step(std::integral_constant<int, 4>{});
+        else if (nrt == 3) step(std::integral_constant<int, 3>{});
+        else if (nrt == 2) step(std::integral_constant<int, 2>{});
         else if (nrt == 1) step(std::integral_constant<int, 1>{});
     }
     __syncthreads();  // every wave is done with the ring before it is reused
@@ -251,13 +240,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     float* T = (float*)smem;
     const int er = tid >> 2, pp = tid & 3;  // output row, 32-column part
     if (MODE == MODE_UP) {
-        for (int rt = 0; rt < 2; rt++) {
-            if (!rt_on[rt]) continue;
-            for (int j = 0; j < 4; j++)
+        for (int rt = 0; rt < 4; rt++) {
+            if (rt >= nrt) continue;  // constant bound keeps acc[] in registers
+            for (int j = 0; j < 2; j++)
                 for (int i = 0; i < 4; i++) {
-                    const float gv = acc[rt][j][i], uv = acc[rt][j + 4][i];
+                    const float gv = acc[rt][j][i], uv = acc[rt][j + 2][i];
                     const float silu = gv / (1.0f + expf(-gv));
-                    T[(32 * wr + 16 * rt + 4 * q + i) * kEpiPitch + 64 * wc + 16 * j + r16] = silu * uv;
+                    T[(64 * wr + 16 * rt + 4 * q + i) * kEpiPitch + 32 * wc + 16 * j + r16] = silu * uv;
                 }
         }
         __syncthreads();
@@ -304,12 +293,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     } else {
         for (int h = 0; h < 2; h++) {
             if (h) __syncthreads();
-            if (wc == h) {
-                for (int rt = 0; rt < 2; rt++) {
-                    if (!rt_on[rt]) continue;
-                    for (int ct = 0; ct < 8; ct++)
+            if ((wc >> 1) == h) {
+                for (int rt = 0; rt < 4; rt++) {
+                    if (rt >= nrt) continue;
+                    for (int ct = 0; ct < 4; ct++)
                         for (int i = 0; i < 4; i++)
-                            T[(32 * wr + 16 * rt + 4 * q + i) * kEpiPitch + 16 * ct + r16] = acc[rt][ct][i];
+                            T[(64 * wr + 16 * rt + 4 * q + i) * kEpiPitch + 64 * (wc & 1) + 16 * ct + r16] =
+                                acc[rt][ct][i];
                 }
             }
             __syncthreads();

@@ -35,6 +35,14 @@ __device__ __forceinline__ int slot_expert(const int* __restrict__ idx, int i, i
     return e;
 }
 
+// First slot k of token t holding expert e, or -1.  A token lists an
+// expert at most once, so token order equals flat slot order t*K+k.
+__device__ __forceinline__ int token_slot_of(const int* __restrict__ row, int K, int e) {
+    for (int k = 0; k < K; k++)
+        if (row[k] == e) return k;
+    return -1;
+}
+
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     const int* __restrict__ idx, int T, int K, int E, int BM, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted_token, int* __restrict__ sorted_slot,
@@ -44,13 +52,19 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     __shared__ int s_red[2];
     const int e = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int P = T * K;
 
     for (int j = tid; j < E; j += kPermThreads) s_hist[j] = 0;
     __syncthreads();
-    for (int i = tid; i < P; i += kPermThreads) {
-        int v = slot_expert(idx, i, K, E);
-        if (v >= 0) atomicAdd(&s_hist[v], 1);
+    // histogram, one token per thread (first occurrence per token only)
+    for (int t = tid; t < T; t += kPermThreads) {
+        const int* row = idx + (size_t)t * K;
+        for (int k = 0; k < K; k++) {
+            const int v = row[k];
+            if (v < 0 || v >= E) continue;
+            bool dup = false;
+            for (int j = 0; j < k; j++) dup |= row[j] == v;
+            if (!dup) atomicAdd(&s_hist[v], 1);
+        }
     }
     __syncthreads();
 
@@ -83,11 +97,12 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     tiles_all = block_sum(tiles_all);
     const int cnt = s_hist[e];
 
-    // stable compaction, chunks of kPermThreads slots in flat order
+    // stable compaction over tokens, chunks of kPermThreads tokens
     int base = 0;
-    for (int c0 = 0; c0 < P; c0 += kPermThreads) {
-        int i = c0 + tid;
-        bool hit = i < P && slot_expert(idx, i, K, E) == e;
+    for (int c0 = 0; c0 < T; c0 += kPermThreads) {
+        const int t = c0 + tid;
+        const int k = t < T ? token_slot_of(idx + (size_t)t * K, K, e) : -1;
+        const bool hit = k >= 0;
         unsigned long long b = __ballot(hit);
         int rank_in_wave = __popcll(b & ((1ull << lane) - 1ull));
         __syncthreads();
@@ -101,8 +116,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
         }
         if (hit) {
             int pos = row_off + base + before + rank_in_wave;
-            sorted_token[pos] = i / K;
-            sorted_slot[pos] = i;
+            sorted_token[pos] = t;
+            sorted_slot[pos] = t * K + k;
         }
         base += total;
     }

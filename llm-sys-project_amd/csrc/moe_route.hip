@@ -26,34 +26,112 @@
 
 namespace amdmoe {
 
-// Routing of one token by one wave.  `p` (LDS) holds E logits and is
-// overwritten with probabilities.  K <= 64.
-__device__ void wave_route_token(float* p, int E, int K, int* out_idx, float* out_wts) {
+// Uniform-index element of a 4-register array (j is wave-uniform).
+__device__ __forceinline__ float pick4(const float (&v)[4], int j) {
+    return j == 0 ? v[0] : (j == 1 ? v[1] : (j == 2 ? v[2] : v[3]));
+}
+
+// Routing of one token by one wave.  `p` (LDS) holds the E logits.
+// E <= 256: the probabilities live in registers (expert e = lane + 64j).
+__device__ void wave_route_token_reg(const float* p, int E, int K, int* out_idx, float* out_wts) {
     const int lane = lane_id();
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? p[e] : -FLT_MAX;
+    }
     // softmax (tests/test_moe.cu:14-20)
+    float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    mx = wave_max(mx);
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? expf(v[j] - mx) : 0.0f;
+    // The denominator is summed in ascending expert order, exactly as the
+    // reference does: lane values are read out one by one (v_readlane).
+    float s = 0.0f;
+    const int nj = (E + 63) / 64;
+    for (int j = 0; j < nj; j++) {
+        const float x = pick4(v, j);
+        const int n = min(64, E - 64 * j);
+        if (n == 64) {
+#pragma unroll
+            for (int l = 0; l < 64; l++)
+                s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+        } else {
+            for (int l = 0; l < n; l++) s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = __fdiv_rn(v[j], s);
+
+    // replace-min top-K.  Lane k < K owns slot k; the first-minimum slot is
+    // found by a reduction over the lowest power of two >= K lanes.
+    int width = 1;
+    while (width < K) width <<= 1;
+    float sv = -FLT_MAX;
+    int si = -1;
+    auto argmin_slot = [&](float& thr) -> int {
+        float mv = lane < K ? sv : INFINITY;
+        int mk = lane < K ? lane : kWave;
+        for (int o = 1; o < width; o <<= 1) {
+            const float ov = __shfl_xor(mv, o, kWave);
+            const int ok = __shfl_xor(mk, o, kWave);
+            if (ov < mv || (ov == mv && ok < mk)) { mv = ov; mk = ok; }
+        }
+        thr = __shfl(mv, 0, kWave);
+        return __shfl(mk, 0, kWave);
+    };
+    float thr;
+    int m = argmin_slot(thr);
+    int pos = 0;
+    while (pos < E) {
+        // first expert e >= pos with p_e > thr: experts are lane-major per
+        // register, so the first register with a hit holds the smallest e
+        int found = E;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            const unsigned long long b = __ballot(e < E && e >= pos && v[j] > thr);
+            if (found == E && b) found = 64 * j + __ffsll(b) - 1;
+        }
+        if (found >= E) break;
+        const float val = __int_as_float(
+            __builtin_amdgcn_readlane(__float_as_int(pick4(v, found >> 6)), found & 63));
+        if (lane == m) { sv = val; si = found; }
+        pos = found + 1;
+        m = argmin_slot(thr);
+    }
+    // renormalise in slot order (tests/test_moe.cu:65-68)
+    float tot = 0.0f;
+    for (int k = 0; k < K; k++) tot = __fadd_rn(tot, __shfl(sv, k, kWave));
+    if (lane < K) {
+        out_idx[lane] = si;
+        out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
+    }
+}
+
+// Generic form for any E: probabilities in LDS (overwrites `p`).
+__device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float* out_wts) {
+    const int lane = lane_id();
     float mx = -FLT_MAX;
     for (int e = lane; e < E; e += kWave) mx = fmaxf(mx, p[e]);
     mx = wave_max(mx);
     for (int e = lane; e < E; e += kWave) p[e] = expf(p[e] - mx);
     wave_lds_sync();
-    // The denominator is summed in ascending expert order, as the reference
-    // does, so p matches it to the last bit whenever expf does.
     float s = 0.0f;
     if (lane == 0)
         for (int e = 0; e < E; e++) s = __fadd_rn(s, p[e]);
     s = __shfl(s, 0, kWave);
     for (int e = lane; e < E; e += kWave) p[e] = __fdiv_rn(p[e], s);
     wave_lds_sync();
-
-    // replace-min top-K.  Lane k < K owns slot k.
     float sv = -FLT_MAX;
     int si = -1;
     auto argmin_slot = [&](float& thr) -> int {
         float v = lane < K ? sv : INFINITY;
         int k = lane < K ? lane : kWave;
         for (int o = 32; o > 0; o >>= 1) {
-            float ov = __shfl_xor(v, o, kWave);
-            int ok = __shfl_xor(k, o, kWave);
+            const float ov = __shfl_xor(v, o, kWave);
+            const int ok = __shfl_xor(k, o, kWave);
             if (ov < v || (ov == v && ok < k)) { v = ov; k = ok; }
         }
         thr = v;
@@ -65,9 +143,8 @@ __device__ void wave_route_token(float* p, int E, int K, int* out_idx, float* ou
     while (pos < E) {
         int found = E;
         for (int c = pos; c < E; c += kWave) {
-            int e = c + lane;
-            bool hit = (e < E) && (p[e] > thr);
-            unsigned long long b = __ballot(hit);
+            const int e = c + lane;
+            const unsigned long long b = __ballot((e < E) && (p[e] > thr));
             if (b) { found = c + __ffsll(b) - 1; break; }
         }
         if (found >= E) break;
@@ -75,14 +152,17 @@ __device__ void wave_route_token(float* p, int E, int K, int* out_idx, float* ou
         pos = found + 1;
         m = argmin_slot(thr);
     }
-    // renormalise in slot order (tests/test_moe.cu:65-68)
     float tot = 0.0f;
     for (int k = 0; k < K; k++) tot = __fadd_rn(tot, __shfl(sv, k, kWave));
     if (lane < K) {
-        float w = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
         out_idx[lane] = si;
-        out_wts[lane] = w;
+        out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
     }
+}
+
+__device__ __forceinline__ void wave_route_token(float* p, int E, int K, int* out_idx, float* out_wts) {
+    if (E <= 256) wave_route_token_reg(p, E, K, out_idx, out_wts);
+    else wave_route_token_lds(p, E, K, out_idx, out_wts);
 }
 
 template <typename T> __device__ __forceinline__ float load_f(const T* p);
@@ -128,89 +208,98 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
 
 // ---------------------------------------------------------------- MFMA
 // bf16 x [T,D] and bf16 Wg [E,D], E <= 256, D % 64 == 0.
-// Block = 512 threads = 8 waves, 32 tokens.  Wave w: token row tile (w & 1),
-// expert column group (w >> 1) of 64 experts (4 MFMA column tiles).
-// K-step = 64 bf16 = 128 bytes per row; LDS rows padded to 144 bytes.
+// Block = 256 threads = 4 waves, 32 tokens; wave w owns experts
+// [64w, 64w+64) (4 MFMA column tiles) for both 16-token row tiles.
+// Each K-step (64 bf16 = 128 bytes of every row) streams the x tile (4 KB)
+// and the whole gate matrix slice (32 KB) global -> LDS through a 3-stage
+// direct-load ring (buffer_load ... lds), so two steps are in flight while
+// one is consumed; rows past T or E read as zeros.  LDS rows are 128 bytes,
+// 16-byte chunks XOR-swizzled by (row & 7).  The gate matrix is re-read by
+// every block from L2; the block count (T/32) keeps that traffic at
+// E*D*2*T/32 bytes.
 constexpr int kRtTok = 32;
-constexpr int kRtPitch = 144;
-constexpr int kRtStage = (kRtTok + 256) * kRtPitch;
+constexpr int kRtStage = (kRtTok + 256) * 128;  // 36864
+constexpr int kRtNS = 3;
+constexpr int kRtLds = kRtNS * kRtStage;        // 110592
 
-__global__ __launch_bounds__(512) void route_mfma_kernel(const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ wg, int T,
-                                                         int E, int K, int D,
-                                                         int* __restrict__ idx,
-                                                         float* __restrict__ wts) {
+__global__ __launch_bounds__(256, 1) void route_mfma_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ wg, int T,
+                                                            int E, int K, int D,
+                                                            int* __restrict__ idx,
+                                                            float* __restrict__ wts) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.x * kRtTok;
     const int nk = D / 64;
-    const size_t row_bytes = (size_t)D * 2;
+    const long row_bytes = (long)D * 2;
 
-    // global -> register staging: x 32 rows * 8 chunks = 256 chunks (threads
-    // < 256), Wg 256 rows * 8 chunks = 2048 chunks (4 per thread).
-    const uint8_t* xsrc = nullptr;
-    int xrow = tid >> 3, xch = tid & 7;
-    if (tid < 256 && t0 + xrow < T) xsrc = (const uint8_t*)x + (size_t)(t0 + xrow) * row_bytes + xch * 16;
-    const uint8_t* wsrc[4];
-    int wrow[4], wch[4];
-    for (int j = 0; j < 4; j++) {
-        int c = tid + 512 * j;
-        wrow[j] = c >> 3;
-        wch[j] = c & 7;
-        wsrc[j] = wrow[j] < E ? (const uint8_t*)wg + (size_t)wrow[j] * row_bytes + wch[j] * 16 : nullptr;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (long)T * row_bytes);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wg, (long)E * row_bytes);
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
+    // x: 4 slabs of 8 rows (one per wave); Wg: 32 slabs (8 per wave)
+    const int xr = t0 + 8 * wave + lrow;
+    const uint32_t voff_x = xr < T ? (uint32_t)(xr * row_bytes + 16 * lchunk) : kOob;
+    uint32_t voff_w[8];
+    for (int j = 0; j < 8; j++) {
+        const int r = 64 * wave + 8 * j + lrow;
+        voff_w[j] = r < E ? (uint32_t)(r * row_bytes + 16 * lchunk) : kOob;
     }
-    u32x4 rx, rw[4];
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    auto gload = [&](int kt) {
-        size_t off = (size_t)kt * 128;
-        rx = xsrc ? *(const u32x4*)(xsrc + off) : zero4;
-        for (int j = 0; j < 4; j++) rw[j] = wsrc[j] ? *(const u32x4*)(wsrc[j] + off) : zero4;
-    };
-    auto sstore = [&](int st) {
+    auto issue = [&](int st, int kt) {
         uint8_t* base = smem + st * kRtStage;
-        if (tid < 256) *(u32x4*)(base + xrow * kRtPitch + xch * 16) = rx;
-        for (int j = 0; j < 4; j++)
-            *(u32x4*)(base + (kRtTok + wrow[j]) * kRtPitch + wch[j] * 16) = rw[j];
+        const int soff = kt * 128;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16, voff_x, soff, 0, 0);
+        for (int j = 0; j < 8; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (lds_ptr_t)(base + (kRtTok + 64 * wave + 8 * j) * 128), 16, voff_w[j], soff, 0, 0);
     };
 
-    f32x4 acc[4];
-    for (int j = 0; j < 4; j++) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int rt = wave & 1, cg = wave >> 1;
-    const bool active = cg * 64 < E;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
+    const bool active = 64 * wave < E;
+    f32x4 acc[2][4];
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
     for (int kt = 0; kt < nk; kt++) {
-        if (kt + 1 < nk) gload(kt + 1);
-        const uint8_t* base = smem + (kt & 1) * kRtStage;
+        if (kt + 1 < nk) wait_vmcnt<9>();
+        else wait_vmcnt<0>();
+        bare_barrier();
+        if (kt + 2 < nk) issue((kt + 2) % kRtNS, kt + 2);
         if (active) {
-            const int q = lane >> 4, r = lane & 15;
-            const uint8_t* ap = base + (rt * 16 + r) * kRtPitch + q * 16;
-            u32x4 a0 = *(const u32x4*)ap, a1 = *(const u32x4*)(ap + 64);
+            const uint8_t* base = smem + (kt % kRtNS) * kRtStage;
+            u32x4 alo[2], ahi[2];
+            for (int rt = 0; rt < 2; rt++) {
+                const uint8_t* p = base + (16 * rt + r16) * 128;
+                alo[rt] = *(const u32x4*)(p + off_lo);
+                ahi[rt] = *(const u32x4*)(p + off_hi);
+            }
             for (int ct = 0; ct < 4; ct++) {
-                const uint8_t* bp = base + (kRtTok + cg * 64 + ct * 16 + r) * kRtPitch + q * 16;
-                u32x4 b0 = *(const u32x4*)bp, b1 = *(const u32x4*)(bp + 64);
-                acc[ct] = mfma_bf16(a0, b0, acc[ct]);
-                acc[ct] = mfma_bf16(a1, b1, acc[ct]);
+                const uint8_t* p = base + (kRtTok + 64 * wave + 16 * ct + r16) * 128;
+                const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
+                for (int rt = 0; rt < 2; rt++) {
+                    acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
+                    acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
+                }
             }
         }
-        if (kt + 1 < nk) sstore((kt + 1) & 1);
-        __syncthreads();
     }
+    __syncthreads();
     // logits -> LDS [32][E]
     float* s_logit = (float*)smem;
     if (active) {
-        const int q = lane >> 4, c = lane & 15;
-        for (int ct = 0; ct < 4; ct++) {
-            int e = cg * 64 + ct * 16 + c;
-            if (e < E)
-                for (int i = 0; i < 4; i++) s_logit[(rt * 16 + q * 4 + i) * E + e] = acc[ct][i];
-        }
+        for (int rt = 0; rt < 2; rt++)
+            for (int ct = 0; ct < 4; ct++) {
+                const int e = 64 * wave + 16 * ct + r16;
+                if (e < E)
+                    for (int i = 0; i < 4; i++) s_logit[(16 * rt + 4 * q + i) * E + e] = acc[rt][ct][i];
+            }
     }
     __syncthreads();
-    for (int lt = wave; lt < kRtTok; lt += 8) {
-        int t = t0 + lt;
+    for (int lt = wave; lt < kRtTok; lt += 4) {
+        const int t = t0 + lt;
         if (t >= T) break;
         wave_route_token(s_logit + lt * E, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
     }
@@ -243,9 +332,7 @@ bool route_mfma_supported(int E, int D) { return E >= 1 && E <= 256 && D % 64 ==
 
 int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
                       float* wts, hipStream_t st) {
-    size_t lds = 2 * (size_t)kRtStage;
-    size_t lds_logit = sizeof(float) * (size_t)kRtTok * E;
-    if (lds_logit > lds) lds = lds_logit;
+    const size_t lds = kRtLds;  // >= the 32 x E fp32 logits of the epilogue
     static bool attr_set = false;
     if (!attr_set) {
         AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)route_mfma_kernel,
@@ -253,7 +340,7 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
         attr_set = true;
     }
     int grid = (int)ceil_div(T, kRtTok);
-    hipLaunchKernelGGL(route_mfma_kernel, dim3(grid), dim3(512), lds, st, x, wg, T, E, K, D, idx,
+    hipLaunchKernelGGL(route_mfma_kernel, dim3(grid), dim3(256), lds, st, x, wg, T, E, K, D, idx,
                        wts);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
