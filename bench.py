@@ -103,10 +103,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=4096)
-    ap.add_argument("--cpu-sample", type=int, default=4, help="tokens for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-sample", type=int, default=256, help="tokens for the CPU baseline (0: skip)")
     ap.add_argument("--skip-dsa", action="store_true")
     ap.add_argument("--traffic", default=None,
                     help="JSON file with measured up-projection HBM bytes per launch")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one 1 GiB device-to-device copy kernel (a known-size "
+                         "reference for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -118,6 +121,12 @@ def main():
     import amdmoe
     import synth
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     T, E, K, D, I = args.tokens, 256, 8, 7168, 2048
     log(f"[bench] generating DSV3 fp8 weights E={E} D={D} I={I}")
     w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=1234)

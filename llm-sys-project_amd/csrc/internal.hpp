@@ -9,7 +9,7 @@ namespace amdmoe {
 enum { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2 };
 enum { MODE_UP = 0, MODE_DOWN = 1 };
 
-constexpr int kMTile = 128;  // rows of one grouped-GEMM M-tile
+constexpr int kMTile = 256;  // rows of one grouped-GEMM M-tile
 
 struct GemmArgs {
     const uint8_t* a;        // A base

@@ -245,8 +245,13 @@ __global__ __launch_bounds__(256, 1) void route_mfma_kernel(const uint16_t* __re
         const int r = 64 * wave + 8 * j + lrow;
         voff_w[j] = r < E ? (uint32_t)(r * row_bytes + 16 * lchunk) : kOob;
     }
+    // rotated K order per block: gate rows are 128-byte slices at a fixed
+    // stride, so blocks in lockstep would all hit the same memory channels
+    const int kt0 = (int)(((unsigned)blockIdx.x * 13u) % (unsigned)nk);
     auto issue = [&](int st, int kt) {
         uint8_t* base = smem + st * kRtStage;
+        kt += kt0;
+        if (kt >= nk) kt -= nk;
         const int soff = kt * 128;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16, voff_x, soff, 0, 0);
         for (int j = 0; j < 8; j++)

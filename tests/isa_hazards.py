@@ -1,0 +1,63 @@
+"""Static check of the grouped GEMM's asm weight loads.
+
+The weight loads of grouped_gemm_kernel are inline-asm
+`buffer_load_dwordx4 v[a:b], ...` (no `lds` modifier): the compiler does not
+know they are still in flight, so nothing may read or overwrite their
+destination registers until an explicit `s_waitcnt vmcnt(...)`.  This walks
+every control-flow path from each such load (following branches) to the
+first vmcnt wait and reports any instruction on the way that names one of
+the destination registers -- a copy, a spill, an MFMA reading it too early,
+or a reuse of the register.
+"""
+import re
+
+
+def _regs(tok):
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"v(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def violations(asm_text):
+    """[(kernel, line, instruction)] for every hazard found."""
+    lines = [ln.split(";")[0].strip() for ln in asm_text.split("\n")]
+    labels = {}
+    for i, ln in enumerate(lines):
+        m = re.match(r"^([.\w]+):$", ln)
+        if m:
+            labels[m.group(1)] = i
+    bad, kern = [], None
+    for i, ln in enumerate(lines):
+        m = re.match(r"^(_Z\w+):$", ln)
+        if m:
+            kern = m.group(1)
+        m = re.match(r"buffer_load_dwordx4 (v\[\d+:\d+\]), ", ln)
+        if not m or ln.endswith(" lds"):
+            continue
+        dst = _regs(m.group(1))
+        stack, seen = [i + 1], set()
+        while stack:
+            j = stack.pop()
+            while j < len(lines) and j not in seen:
+                seen.add(j)
+                t = lines[j]
+                if t.startswith("s_waitcnt") and "vmcnt" in t:
+                    break
+                if t.startswith("s_endpgm"):
+                    bad.append((kern, i + 1, "reaches s_endpgm with the load in flight"))
+                    break
+                if t.startswith("s_branch"):
+                    j = labels[t.split()[1]]
+                    continue
+                if t.startswith("s_cbranch"):
+                    stack.append(labels[t.split()[1]])
+                if t and not t.endswith(":") and not t.startswith(".") \
+                        and not t.startswith("buffer_load_dwordx4"):
+                    ops = re.split(r"[ ,]+", t)[1:]
+                    if set().union(set(), *[_regs(o) for o in ops]) & dst:
+                        bad.append((kern, j + 1, t))
+                        break
+                j += 1
+    return bad

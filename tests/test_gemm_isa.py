@@ -1,0 +1,44 @@
+"""The grouped GEMM's in-flight weight registers are never touched before
+their wait (see tests/isa_hazards.py), checked on the gfx950 assembly of
+csrc/moe_gemm.hip as the library's Makefile compiles it."""
+import os
+import shutil
+import subprocess
+
+import pytest
+
+from isa_hazards import violations
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SRC = os.path.join(ROOT, "llm-sys-project_amd", "csrc", "moe_gemm.hip")
+HIPCC = "/opt/rocm/bin/hipcc"
+
+
+def test_checker_flags_a_copy_before_the_wait():
+    asm = "\n".join([
+        "_Zk:", "\tbuffer_load_dwordx4 v[2:5], v1, s[0:3], s4 offen offset:0",
+        "\tv_mov_b32_e32 v9, v3", "\ts_waitcnt vmcnt(0)", "\ts_endpgm"])
+    assert len(violations(asm)) == 1
+    clean = asm.replace("\tv_mov_b32_e32 v9, v3\n\ts_waitcnt vmcnt(0)", "\ts_waitcnt vmcnt(0)\n\tv_mov_b32_e32 v9, v3")
+    assert violations(clean) == []
+
+
+def test_checker_follows_branches_to_a_use():
+    asm = "\n".join([
+        "_Zk:", "\tbuffer_load_dwordx4 v[2:5], v1, s[0:3], s4 offen offset:0",
+        "\ts_cbranch_scc1 .LBB0_2", "\ts_waitcnt vmcnt(0)", ".LBB0_2:",
+        "\tv_add_u32_e32 v4, v6, v7", "\ts_waitcnt vmcnt(0)", "\ts_endpgm"])
+    assert len(violations(asm)) == 1
+
+
+@pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc missing")
+def test_grouped_gemm_weight_loads_are_never_touched_in_flight(tmp_path):
+    out = tmp_path / "moe_gemm.s"
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                    "--cuda-device-only", "-S", SRC, "-o", str(out)],
+                   check=True, capture_output=True)
+    asm = out.read_text()
+    assert asm.count("buffer_load_dwordx4 v[") > 0
+    bad = violations(asm)
+    assert bad == [], bad[:5]
