@@ -48,6 +48,7 @@ struct MoeWs {
     uint8_t* act;
     float* act_s;
     uint8_t* ypair;
+    float* logits;  // gate logits scratch of the MFMA routing (fp8 path)
     size_t total;
 };
 
@@ -79,6 +80,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
         w.act = take(P * I);
         w.act_s = (float*)take(4 * P * (I / 128));
         w.ypair = take(2 * P * D);
+        w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E));
     } else {
         const size_t es = elem_size(dtype);
         w.act = take(es * P * I);
@@ -287,7 +289,7 @@ int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const
     TRY(mark(0, st));
     if (route_mfma_supported(c.num_experts, c.hidden_dim))
         TRY(launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
-                              w.idx, w.wts, st));
+                              w.idx, w.wts, w.logits, st));
     else
         TRY(launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, c.num_tokens,
                                                    c.num_experts, c.top_k, c.hidden_dim, w.idx,
@@ -322,10 +324,14 @@ int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* ex
                          float* expert_weights, const MoeConfig* cfg, void* stream) {
     TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
     if (cfg->num_tokens == 0) return AMDMOE_OK;
-    if (route_mfma_supported(cfg->num_experts, cfg->hidden_dim))
+    if (route_mfma_supported(cfg->num_experts, cfg->hidden_dim)) {
+        // logits scratch: the library's cached per-device workspace
+        void* scratch = nullptr;
+        TRY(cached_workspace(route_mfma_scratch_bytes(cfg->num_tokens, cfg->num_experts), &scratch));
         return launch_route_mfma(x, gate_weight, cfg->num_tokens, cfg->num_experts, cfg->top_k,
-                                 cfg->hidden_dim, expert_indices, expert_weights,
+                                 cfg->hidden_dim, expert_indices, expert_weights, (float*)scratch,
                                  (hipStream_t)stream);
+    }
     return launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, cfg->num_tokens,
                                                   cfg->num_experts, cfg->top_k, cfg->hidden_dim,
                                                   expert_indices, expert_weights,

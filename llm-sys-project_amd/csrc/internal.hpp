@@ -39,8 +39,10 @@ template <typename XT, typename GT>
 int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int E, int K, int D,
                        int* idx, float* wts, hipStream_t st);
 bool route_mfma_supported(int E, int D);
+// logits: scratch of route_mfma_scratch_bytes(T, E)
+size_t route_mfma_scratch_bytes(int T, int E);
 int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
-                      float* wts, hipStream_t st);
+                      float* wts, float* logits, hipStream_t st);
 
 // moe_permute.hip
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,

@@ -31,16 +31,26 @@ __device__ __forceinline__ float pick4(const float (&v)[4], int j) {
     return j == 0 ? v[0] : (j == 1 ? v[1] : (j == 2 ? v[2] : v[3]));
 }
 
-// Routing of one token by one wave.  `p` (LDS) holds the E logits.
-// E <= 256: the probabilities live in registers (expert e = lane + 64j).
-__device__ void wave_route_token_reg(const float* p, int E, int K, int* out_idx, float* out_wts) {
+// min over lanes [0, width) of a row of 16 lanes (width a power of two <= 16),
+// by DPP within the row: xor 1, xor 2 (quad permutes), then the half-row and
+// full-row mirrors pair every lane of one group with one of the other.
+// Lanes outside [0, width) must hold +inf.
+template <int CTRL>
+__device__ __forceinline__ float dpp_min(float v) {
+    return fminf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float row_min16(float v, int width) {
+    v = dpp_min<0xB1>(v);                  // quad_perm [1,0,3,2]
+    if (width > 2) v = dpp_min<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (width > 4) v = dpp_min<0x141>(v);  // row_half_mirror
+    if (width > 8) v = dpp_min<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Routing of one token by one wave, E <= 256: `v` holds the logits of
+// experts lane + 64j (j < 4; -FLT_MAX past E).
+__device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, float* out_wts) {
     const int lane = lane_id();
-    float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? p[e] : -FLT_MAX;
-    }
     // softmax (tests/test_moe.cu:14-20)
     float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
     mx = wave_max(mx);
@@ -64,22 +74,24 @@ __device__ void wave_route_token_reg(const float* p, int E, int K, int* out_idx,
 #pragma unroll
     for (int j = 0; j < 4; j++) v[j] = __fdiv_rn(v[j], s);
 
-    // replace-min top-K.  Lane k < K owns slot k; the first-minimum slot is
-    // found by a reduction over the lowest power of two >= K lanes.
-    int width = 1;
-    while (width < K) width <<= 1;
+    // replace-min top-K.  Lane k < K owns slot k.  The victim is the first
+    // slot holding the smallest value: its value comes from a DPP min over
+    // the slot lanes (K <= 16) and its position from a ballot of the lanes
+    // equal to it.
     float sv = -FLT_MAX;
     int si = -1;
     auto argmin_slot = [&](float& thr) -> int {
-        float mv = lane < K ? sv : INFINITY;
-        int mk = lane < K ? lane : kWave;
-        for (int o = 1; o < width; o <<= 1) {
-            const float ov = __shfl_xor(mv, o, kWave);
-            const int ok = __shfl_xor(mk, o, kWave);
-            if (ov < mv || (ov == mv && ok < mk)) { mv = ov; mk = ok; }
+        const float mine = lane < K ? sv : INFINITY;
+        float mv;
+        if (K <= 16) {
+            mv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(row_min16(mine, K))));
+        } else {
+            mv = mine;
+            for (int o = 1; o < kWave; o <<= 1) mv = fminf(mv, __shfl_xor(mv, o, kWave));
+            mv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mv)));
         }
-        thr = __shfl(mv, 0, kWave);
-        return __shfl(mk, 0, kWave);
+        thr = mv;
+        return __ffsll(__ballot(lane < K && sv == mv)) - 1;
     };
     float thr;
     int m = argmin_slot(thr);
@@ -103,7 +115,8 @@ __device__ void wave_route_token_reg(const float* p, int E, int K, int* out_idx,
     }
     // renormalise in slot order (tests/test_moe.cu:65-68)
     float tot = 0.0f;
-    for (int k = 0; k < K; k++) tot = __fadd_rn(tot, __shfl(sv, k, kWave));
+    for (int k = 0; k < K; k++)
+        tot = __fadd_rn(tot, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), k)));
     if (lane < K) {
         out_idx[lane] = si;
         out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
@@ -161,8 +174,15 @@ __device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float
 }
 
 __device__ __forceinline__ void wave_route_token(float* p, int E, int K, int* out_idx, float* out_wts) {
-    if (E <= 256) wave_route_token_reg(p, E, K, out_idx, out_wts);
-    else wave_route_token_lds(p, E, K, out_idx, out_wts);
+    if (E <= 256) {
+        const int lane = lane_id();
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? p[lane + 64 * j] : -FLT_MAX;
+        wave_route_token_reg(v, E, K, out_idx, out_wts);
+    } else {
+        wave_route_token_lds(p, E, K, out_idx, out_wts);
+    }
 }
 
 template <typename T> __device__ __forceinline__ float load_f(const T* p);
@@ -207,42 +227,45 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
 }
 
 // ---------------------------------------------------------------- MFMA
-// bf16 x [T,D] and bf16 Wg [E,D], E <= 256, D % 64 == 0.
-// Block = 256 threads = 4 waves, 32 tokens; wave w owns experts
-// [64w, 64w+64) (4 MFMA column tiles) for both 16-token row tiles.
-// Each K-step (64 bf16 = 128 bytes of every row) streams the x tile (4 KB)
-// and the whole gate matrix slice (32 KB) global -> LDS through a 3-stage
-// direct-load ring (buffer_load ... lds), so two steps are in flight while
-// one is consumed; rows past T or E read as zeros.  LDS rows are 128 bytes,
-// 16-byte chunks XOR-swizzled by (row & 7).  The gate matrix is re-read by
-// every block from L2; the block count (T/32) keeps that traffic at
-// E*D*2*T/32 bytes.
+// bf16 x [T,D] and bf16 Wg [E,D], E <= 256, D % 64 == 0.  Two launches:
+//
+// route_logits_kernel: the gate GEMM, logits [T,E] fp32 into a scratch
+//   buffer.  Block = 256 threads, a 32-token x 128-expert tile (wave w owns
+//   experts [32w, 32w+32): 2 row tiles x 2 column tiles of 16x16 MFMA).
+//   Each K-step (64 bf16 = 128 bytes of every row) streams the x rows (4 KB)
+//   and the gate rows (16 KB) global -> LDS through a 3-stage direct-load
+//   ring, so two steps are in flight while one is consumed; rows past T or E
+//   read as zeros.  LDS rows are 128 bytes, 16-byte chunks XOR-swizzled by
+//   (row & 7).  With T/32 x E/128 blocks (256 at T=4096, E=256) every CU
+//   streams; the gate matrix is re-read per token tile from L2.
+// route_topk_kernel: one wave per token (softmax + replace-min top-K +
+//   renormalisation, wave_route_token_reg), 4 tokens per block, so a CU
+//   interleaves many tokens' latency-bound shuffle chains.
 constexpr int kRtTok = 32;
-constexpr int kRtStage = (kRtTok + 256) * 128;  // 36864
+constexpr int kRtExp = 128;
+constexpr int kRtStage = (kRtTok + kRtExp) * 128;  // 20480
 constexpr int kRtNS = 3;
-constexpr int kRtLds = kRtNS * kRtStage;        // 110592
+constexpr int kRtLds = kRtNS * kRtStage;           // 61440
 
-__global__ __launch_bounds__(256, 1) void route_mfma_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ wg, int T,
-                                                            int E, int K, int D,
-                                                            int* __restrict__ idx,
-                                                            float* __restrict__ wts) {
+__global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ wg, int T,
+                                                           int E, int D, float* __restrict__ logits) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t0 = blockIdx.x * kRtTok;
+    const int t0 = blockIdx.x * kRtTok, e0 = blockIdx.y * kRtExp;
     const int nk = D / 64;
     const long row_bytes = (long)D * 2;
 
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (long)T * row_bytes);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wg, (long)E * row_bytes);
     const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
-    // x: 4 slabs of 8 rows (one per wave); Wg: 32 slabs (8 per wave)
+    // x: 4 slabs of 8 rows (one per wave); Wg: 16 slabs (4 per wave)
     const int xr = t0 + 8 * wave + lrow;
     const uint32_t voff_x = xr < T ? (uint32_t)(xr * row_bytes + 16 * lchunk) : kOob;
-    uint32_t voff_w[8];
-    for (int j = 0; j < 8; j++) {
-        const int r = 64 * wave + 8 * j + lrow;
+    uint32_t voff_w[4];
+    for (int j = 0; j < 4; j++) {
+        const int r = e0 + 32 * wave + 8 * j + lrow;
         voff_w[j] = r < E ? (uint32_t)(r * row_bytes + 16 * lchunk) : kOob;
     }
     // rotated K order per block: gate rows are 128-byte slices at a fixed
@@ -254,60 +277,62 @@ __global__ __launch_bounds__(256, 1) void route_mfma_kernel(const uint16_t* __re
         if (kt >= nk) kt -= nk;
         const int soff = kt * 128;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16, voff_x, soff, 0, 0);
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < 4; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (lds_ptr_t)(base + (kRtTok + 64 * wave + 8 * j) * 128), 16, voff_w[j], soff, 0, 0);
+                rw, (lds_ptr_t)(base + (kRtTok + 32 * wave + 8 * j) * 128), 16, voff_w[j], soff, 0, 0);
     };
 
     const int q = lane >> 4, r16 = lane & 15;
     const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
-    const bool active = 64 * wave < E;
-    f32x4 acc[2][4];
+    f32x4 acc[2][2];
     for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 4; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     issue(0, 0);
     if (nk > 1) issue(1, 1);
     for (int kt = 0; kt < nk; kt++) {
-        if (kt + 1 < nk) wait_vmcnt<9>();
+        if (kt + 1 < nk) wait_vmcnt<5>();
         else wait_vmcnt<0>();
         bare_barrier();
         if (kt + 2 < nk) issue((kt + 2) % kRtNS, kt + 2);
-        if (active) {
-            const uint8_t* base = smem + (kt % kRtNS) * kRtStage;
-            u32x4 alo[2], ahi[2];
+        const uint8_t* base = smem + (kt % kRtNS) * kRtStage;
+        u32x4 alo[2], ahi[2];
+        for (int rt = 0; rt < 2; rt++) {
+            const uint8_t* p = base + (16 * rt + r16) * 128;
+            alo[rt] = *(const u32x4*)(p + off_lo);
+            ahi[rt] = *(const u32x4*)(p + off_hi);
+        }
+        for (int ct = 0; ct < 2; ct++) {
+            const uint8_t* p = base + (kRtTok + 32 * wave + 16 * ct + r16) * 128;
+            const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
             for (int rt = 0; rt < 2; rt++) {
-                const uint8_t* p = base + (16 * rt + r16) * 128;
-                alo[rt] = *(const u32x4*)(p + off_lo);
-                ahi[rt] = *(const u32x4*)(p + off_hi);
-            }
-            for (int ct = 0; ct < 4; ct++) {
-                const uint8_t* p = base + (kRtTok + 64 * wave + 16 * ct + r16) * 128;
-                const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
-                for (int rt = 0; rt < 2; rt++) {
-                    acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
-                    acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
-                }
+                acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
+                acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
             }
         }
     }
-    __syncthreads();
-    // logits -> LDS [32][E]
-    float* s_logit = (float*)smem;
-    if (active) {
-        for (int rt = 0; rt < 2; rt++)
-            for (int ct = 0; ct < 4; ct++) {
-                const int e = 64 * wave + 16 * ct + r16;
-                if (e < E)
-                    for (int i = 0; i < 4; i++) s_logit[(16 * rt + 4 * q + i) * E + e] = acc[rt][ct][i];
+    // lane (q, r16) holds logits of tokens 16rt + 4q + i, expert 16ct + r16
+    for (int rt = 0; rt < 2; rt++)
+        for (int ct = 0; ct < 2; ct++) {
+            const int e = e0 + 32 * wave + 16 * ct + r16;
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + 16 * rt + 4 * q + i;
+                if (e < E && t < T) logits[(size_t)t * E + e] = acc[rt][ct][i];
             }
-    }
-    __syncthreads();
-    for (int lt = wave; lt < kRtTok; lt += 4) {
-        const int t = t0 + lt;
-        if (t >= T) break;
-        wave_route_token(s_logit + lt * E, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
-    }
+        }
+}
+
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T,
+                                                         int E, int K, int* __restrict__ idx,
+                                                         float* __restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;  // whole wave
+    const float* row = logits + (size_t)t * E;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? row[lane + 64 * j] : -FLT_MAX;
+    wave_route_token_reg(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
 // ---------------------------------------------------------------- launch
@@ -335,18 +360,16 @@ template int launch_route_exact<uint16_t, uint16_t>(const uint16_t*, const uint1
 
 bool route_mfma_supported(int E, int D) { return E >= 1 && E <= 256 && D % 64 == 0; }
 
+size_t route_mfma_scratch_bytes(int T, int E) { return (size_t)T * E * sizeof(float); }
+
 int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
-                      float* wts, hipStream_t st) {
-    const size_t lds = kRtLds;  // >= the 32 x E fp32 logits of the epilogue
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)route_mfma_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr_set = true;
-    }
-    int grid = (int)ceil_div(T, kRtTok);
-    hipLaunchKernelGGL(route_mfma_kernel, dim3(grid), dim3(256), lds, st, x, wg, T, E, K, D, idx,
-                       wts);
+                      float* wts, float* logits, hipStream_t st) {
+    AMDMOE_CHECK_ARG(route_mfma_supported(E, D), "routing: MFMA gate needs E <= 256 and D %% 64 == 0");
+    dim3 g1((unsigned)ceil_div(T, kRtTok), (unsigned)ceil_div(E, kRtExp));
+    hipLaunchKernelGGL(route_logits_kernel, g1, dim3(256), kRtLds, st, x, wg, T, E, D, logits);
+    AMDMOE_LAUNCH_CHECK();
+    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, logits,
+                       T, E, K, idx, wts);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
