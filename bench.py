@@ -103,7 +103,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tokens", type=int, default=4096)
-    ap.add_argument("--cpu-sample", type=int, default=256, help="tokens for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-sample", type=int, default=1024, help="tokens for the CPU baseline (0: skip)")
     ap.add_argument("--skip-dsa", action="store_true")
     ap.add_argument("--traffic", default=None,
                     help="JSON file with measured up-projection HBM bytes per launch")

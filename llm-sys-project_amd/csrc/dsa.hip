@@ -117,6 +117,29 @@ constexpr int kDsaLds = kRowsOff + kMaxS * 4;    // 126976
 constexpr int kLoadsPerWave = kStageB / 1024 / 4;  // 9
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Reductions over the lanes l, l^16 (resp. l^32) with the gfx950 lane
+// swaps: permlane16_swap exchanges the odd 16-lane rows of its first operand
+// with the even rows of its second, permlane32_swap the upper half of the
+// first with the lower half of the second; with both operands the same
+// value the two results hold, at every lane, the values of l and l^16
+// (resp. l^32) in some order.
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
@@ -158,14 +181,24 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     __syncthreads();  // s_rows visible; regular loads complete
 
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
+    // Lane chunk n of this wave's share of a stage: chunk c = 64*(9w+n)+lane
+    // of the 32x72-chunk tile, row c / 72, swizzled column.  The 9 physical
+    // rows are read from LDS together, then the 9 loads go out.
     auto issue = [&](int st, int tile) {
         uint8_t* base = smem + st * kStageB;
+        int row[kLoadsPerWave];
+#pragma unroll
         for (int n = 0; n < kLoadsPerWave; n++) {
-            const int c = 64 * (kLoadsPerWave * wave + n) + lane;  // chunk position in the stage
+            const int c = 64 * (kLoadsPerWave * wave + n) + lane;
+            const int tok = tile * kTileTok + c / kRowChunks;
+            row[n] = tok < S ? s_rows[tok] : -1;
+        }
+#pragma unroll
+        for (int n = 0; n < kLoadsPerWave; n++) {
+            const int c = 64 * (kLoadsPerWave * wave + n) + lane;
             const int r = c / kRowChunks, jp = c - r * kRowChunks;
-            const int tok = tile * kTileTok + r;
             const int j = jp ^ (r & 7);
-            const uint32_t vo = tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * j) : kOob;
+            const uint32_t vo = row[n] >= 0 ? (uint32_t)((long)row[n] * kRowBytes + 16 * j) : kOob;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc, (lds_ptr_t)(base + 1024 * (kLoadsPerWave * wave + n)), 16, vo, 0, 0, 0);
         }
@@ -193,13 +226,23 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
         if (t + 2 < ntiles) issue((t + 2) % kDsaNS, t + 2);
         const uint8_t* kb = smem + (t % kDsaNS) * kStageB;
 
-        // S^T: two independent accumulation chains over the 18 K-steps
+        // S^T: two independent accumulation chains over the 18 K-steps; the
+        // K fragments are read from LDS four steps ahead of their MFMA
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb2 = {0.f, 0.f, 0.f, 0.f};
-        for (int ks = 0; ks < 18; ks += 2) {
-            const u32x4 a0 = *(const u32x4*)(kb + r_s * kRowBytes + 16 * ((4 * ks + g) ^ (r_s & 7)));
-            const u32x4 a1 = *(const u32x4*)(kb + r_s * kRowBytes + 16 * ((4 * ks + 4 + g) ^ (r_s & 7)));
-            sa = mfma_bf16(a0, qf[ks], sa);
-            sb2 = mfma_bf16(a1, qf[ks + 1], sb2);
+        {
+            const uint8_t* krow = kb + r_s * kRowBytes;
+            auto kfrag = [&](int ks) __attribute__((always_inline)) {
+                return *(const u32x4*)(krow + 16 * ((4 * ks + g) ^ (r_s & 7)));
+            };
+            u32x4 a[18];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) a[ks] = kfrag(ks);
+#pragma unroll
+            for (int ks = 0; ks < 18; ks++) {
+                if (ks + 4 < 18) a[ks + 4] = kfrag(ks + 4);
+                if (ks & 1) sb2 = mfma_bf16(a[ks], qf[ks], sb2);
+                else sa = mfma_bf16(a[ks], qf[ks], sa);
+            }
         }
         // lane: head c16, tokens 16th + 4g + i of this tile
         float sv[4];
@@ -209,8 +252,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
             sv[i] = tk < S ? (sa[i] + sb2[i]) * scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, sv[i]);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = xor16_max(tmax);
+        tmax = xor32_max(tmax);
         const bool raise = tmax > m_run + 8.0f;
         if (__ballot(raise)) {  // rare after the first tile: rescale O
             const float m_new = raise ? tmax : m_run;
@@ -225,17 +268,26 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
             pv[i] = sv[i] == -INFINITY ? 0.0f : exp2f(sv[i] - m_run);
             psum += pv[i];
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = xor16_sum(psum);
+        psum = xor32_sum(psum);
         l_run += psum;
         const u32x2 pb2 = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
         const s16x4 pb = __builtin_bit_cast(s16x4, pb2);
+        {
+            const uint8_t* vrow = kb + r_v * kRowBytes;
+            auto vfrag = [&](int mt) __attribute__((always_inline)) {
+                const int dd = 16 * mt + vsub;
+                return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4_ptr)(vrow + 16 * ((dd >> 3) ^ (r_v & 7)) + 8 * ((dd >> 2) & 1)));
+            };
+            s16x4 va[32];
 #pragma unroll
-        for (int mt = 0; mt < 32; mt++) {
-            const int dd = 16 * mt + vsub;
-            const uint8_t* va = kb + r_v * kRowBytes + 16 * ((dd >> 3) ^ (r_v & 7)) + 8 * ((dd >> 2) & 1);
-            const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(va));
-            o[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb, o[mt], 0, 0, 0);
+            for (int mt = 0; mt < 6; mt++) va[mt] = vfrag(mt);
+#pragma unroll
+            for (int mt = 0; mt < 32; mt++) {
+                if (mt + 6 < 32) va[mt + 6] = vfrag(mt + 6);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[mt], pb, o[mt], 0, 0, 0);
+            }
         }
     }
     __syncthreads();  // ring no longer read; reuse it for the merge
