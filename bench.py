@@ -105,8 +105,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--cpu-sample", type=int, default=1024, help="tokens for the CPU baseline (0: skip)")
     ap.add_argument("--skip-dsa", action="store_true")
-    ap.add_argument("--traffic", default=None,
-                    help="JSON file with measured up-projection HBM bytes per launch")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "moe_dsv3_fp8_T4096_traffic.json"),
+                    help="measured HBM bytes per launch (FETCH_SIZE/WRITE_SIZE counter runs, "
+                         "calibrated on a copy kernel; see the .md beside it)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 1 GiB device-to-device copy kernel (a known-size "
                          "reference for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -167,8 +168,8 @@ def main():
     up_ms = per_stage["gemm_up"]
     achieved = up_bytes / (up_ms * 1e-3) / 1e9
     traffic = None
-    if args.traffic and os.path.exists(args.traffic):
-        traffic = json.load(open(args.traffic)).get("gemm_up_bytes")
+    if args.traffic and os.path.exists(args.traffic) and T == 4096:
+        traffic = json.load(open(args.traffic))["kernels"].get("grouped_gemm_kernel<fp8, UP>", {}).get("bytes")
     result = {
         "metric": METRIC,
         "value": round(T / (ms * 1e-3), 1),
@@ -191,7 +192,7 @@ def main():
         "roofline": {"kernel": "grouped_gemm_kernel<fp8, up> (GEMM1 + SwiGLU + requant)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),
-                     "traffic": traffic, "algorithmic_bytes": up_bytes},
+                     "traffic": round(traffic) if traffic else None, "algorithmic_bytes": up_bytes},
     }
     if not args.skip_dsa:
         log("[bench] DSA decode")

@@ -211,9 +211,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         }
     }
 
-    // K-steps run in a rotated order starting at kt0 so that concurrent
-    // workgroups do not walk the same K slices in lockstep.
-    const int kt0 = (int)(((unsigned)w * 7u) % (unsigned)nk);
+    // K-steps run in a rotated order starting at kt0, keyed by the M-tile:
+    // the N-tiles of one M-tile run together on one XCD and read the same
+    // activation K-slice at the same time (one fetch, the rest L2 hits),
+    // while different M-tiles start at different K offsets.
+    const int kt0 = (int)(((unsigned)mt * 7u) % (unsigned)nk);
     auto kblk = [&](int kt) __attribute__((always_inline)) {
         int k = kt + kt0;
         k = k >= nk ? k - nk : k;
