@@ -148,20 +148,34 @@ def main():
         amdmoe.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, cfg, ws=ws)
     torch.cuda.synchronize()
 
-    log(f"[bench] timing {args.steps} steps")
-    stage = [amdmoe.StageEvents() for _ in range(args.steps)]
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    for i in range(args.steps):
-        stage[i].arm()
-        amdmoe.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, cfg, ws=ws)
-    t1.record()
-    amdmoe.StageEvents.disarm()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
-    per_stage = {n: sum(s.stage_ms()[n] for s in stage) / args.steps for n in amdmoe.StageEvents.NAMES}
-    log("[bench] stage ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per_stage.items()))
+    def timed(forward):
+        stage = [amdmoe.StageEvents() for _ in range(args.steps)]
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for i in range(args.steps):
+            stage[i].arm()
+            forward()
+        t1.record()
+        amdmoe.StageEvents.disarm()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+        per_stage = {n: sum(s.stage_ms()[n] for s in stage) / args.steps for n in amdmoe.StageEvents.NAMES}
+        log(f"[bench] {ms:.4f} ms/step; stage ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per_stage.items()))
+        return ms, per_stage
+
+    log(f"[bench] timing {args.steps} steps (row-major weights, the drop-in layout)")
+    ms, per_stage = timed(lambda: amdmoe.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y, cfg, ws=ws))
+
+    # the same layer with the expert weights packed once into fragment-block order
+    w1p, w2p = torch.empty_like(w1q), torch.empty_like(w2q)
+    amdmoe.pack_weights_fp8(w1q, w1p)
+    amdmoe.pack_weights_fp8(w2q, w2p)
+    for _ in range(args.warmup):
+        amdmoe.moe_forward_fp8_packed(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=ws)
+    log(f"[bench] timing {args.steps} steps (packed weights)")
+    ms_p, per_stage_p = timed(lambda: amdmoe.moe_forward_fp8_packed(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=ws))
+    del w1p, w2p
 
     flops = 6 * T * K * D * I
     layer_bytes, up_bytes = moe_bytes(T, e_active, K, D, I)
@@ -189,6 +203,11 @@ def main():
         "fp8_peak_frac": round(flops / (ms * 1e-3) / FP8_PEAK, 4),
         "layer_hbm_frac": round(layer_bytes / (ms * 1e-3) / HBM_PEAK, 4),
         "stage_ms": {k: round(v, 4) for k, v in per_stage.items()},
+        "packed_weights": {"note": "same layer, W1/W2 repacked once at load into MFMA "
+                                   "fragment-block order (amdmoe_pack_weights_fp8)",
+                           "value": round(T / (ms_p * 1e-3), 1), "ms_per_step": round(ms_p, 4),
+                           "fp8_peak_frac": round(flops / (ms_p * 1e-3) / FP8_PEAK, 4),
+                           "stage_ms": {k: round(v, 4) for k, v in per_stage_p.items()}},
         "roofline": {"kernel": "grouped_gemm_kernel<fp8, up> (GEMM1 + SwiGLU + requant)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),

@@ -99,6 +99,26 @@ int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const
                            uint16_t* y, const MoeConfig* cfg, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* The fp8 layer with pre-packed expert weights.  No counterpart in the
+ * reference (whose moe_forward, naive_moe.cuh:74-76, is fp32 only): the
+ * same computation and arguments as amdmoe_moe_forward_fp8, but W1 and W2
+ * are given in the fragment-block order written by amdmoe_pack_weights_fp8
+ * (scales unchanged).  Results are bit-identical to the row-major entry. */
+int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight,
+                                  const uint8_t* w1_packed, const float* w1_scale,
+                                  const uint8_t* w2_packed, const float* w2_scale, uint16_t* y,
+                                  const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* One-time repacking of row-major expert weights [num_experts][rows][cols]
+ * (bytes; W1 [E,2I,D] or W2 [E,D,I] e4m3, naive_moe.cuh:66-72) into
+ * fragment-block order: per expert, per 16 rows x 128 bytes, 2 KB stored as
+ * [half h][lane l][16 B] with lane l = 16q + r holding row r, bytes
+ * 64h + 16q .. +15 of the block; blocks ordered [rows/16][cols/128].  Needs
+ * rows % 16 == 0 and cols % 128 == 0; out must not alias w. */
+int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int cols, uint8_t* out,
+                            void* stream);
+
 /* --- stage entry points with the reference's semantics --- */
 
 /* Routing: replaces moe_gate (naive_moe.cuh:27-29, naive_moe.cu:341-355).

@@ -18,6 +18,7 @@ AMDMOE_DTYPE_FP8 = 2
 SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
     "amdmoe_moe_forward_f32", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
+    "amdmoe_moe_forward_fp8_packed", "amdmoe_pack_weights_fp8",
     "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
@@ -67,6 +68,8 @@ def load():
         "amdmoe_moe_forward_f32": (I, [_P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_bf16": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_moe_forward_fp8_packed": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_pack_weights_fp8": (I, [_P, I, I, I, _P, _P]),
         "amdmoe_moe_gate_f32": (I, [_P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16x": (I, [_P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16": (I, [_P, _P, _P, _P, cfgp, _P]),
@@ -148,6 +151,21 @@ def moe_forward_fp8(x, wg, w1, w1s, w2, w2s, y, cfg, ws=None, stream=None):
     _check(load().amdmoe_moe_forward_fp8(_ptr(x), _ptr(wg), _ptr(w1), _ptr(w1s), _ptr(w2),
                                          _ptr(w2s), _ptr(y), ctypes.byref(cfg), p, n,
                                          _stream(stream)))
+
+
+def moe_forward_fp8_packed(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=None, stream=None):
+    """amdmoe_moe_forward_fp8 with W1/W2 in pack_weights_fp8 order."""
+    p, n = _ws(ws)
+    _check(load().amdmoe_moe_forward_fp8_packed(_ptr(x), _ptr(wg), _ptr(w1p), _ptr(w1s), _ptr(w2p),
+                                                _ptr(w2s), _ptr(y), ctypes.byref(cfg), p, n,
+                                                _stream(stream)))
+
+
+def pack_weights_fp8(w, out, stream=None):
+    """Repack e4m3 expert weights w [E, rows, cols] (uint8 device tensor) into out (same shape
+    and size) in fragment-block order."""
+    E, rows, cols = w.shape
+    _check(load().amdmoe_pack_weights_fp8(_ptr(w), E, rows, cols, _ptr(out), _stream(stream)))
 
 
 def moe_gate_f32(x, wg, idx, wts, cfg, stream=None):

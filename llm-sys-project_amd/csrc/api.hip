@@ -156,7 +156,8 @@ static int resolve_ws(const MoeConfig& c, int dtype, void* workspace, size_t byt
 // Shared tail of every forward: permute, both grouped GEMMs, combine.
 static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t* a_x,
                        const float* x_scale, const uint8_t* w1, const float* w1s,
-                       const uint8_t* w2, const float* w2s, void* y, hipStream_t st) {
+                       const uint8_t* w2, const float* w2s, void* y, hipStream_t st,
+                       bool packed = false) {
     const int T = c.num_tokens, E = c.num_experts, K = c.top_k, D = c.hidden_dim,
               I = c.intermediate_dim;
     const long P = (long)T * K;
@@ -175,6 +176,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     up.b = w1;
     up.b_expert_bytes = 2L * I * D * es;
     up.b_row_bytes = (long)D * es;
+    up.b_packed = packed;
     up.b_scale = w1s;
     up.b_rows = 2 * I;
     up.K = D;
@@ -195,6 +197,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.b = w2;
     dn.b_expert_bytes = (long)D * I * es;
     dn.b_row_bytes = (long)I * es;
+    dn.b_packed = packed;
     dn.b_scale = w2s;
     dn.b_rows = D;
     dn.K = I;
@@ -274,10 +277,10 @@ int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const f
                        (const uint8_t*)w2, nullptr, y, st);
 }
 
-int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
-                           const float* w1_scale, const uint8_t* w2, const float* w2_scale,
-                           uint16_t* y, const MoeConfig* cfg, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+static int forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
+                       const float* w1_scale, const uint8_t* w2, const float* w2_scale,
+                       uint16_t* y, const MoeConfig* cfg, void* workspace,
+                       size_t workspace_bytes, void* stream, bool packed) {
     TRY(check_cfg(cfg, AMDMOE_DTYPE_FP8));
     const MoeConfig& c = *cfg;
     if (c.num_tokens == 0) return AMDMOE_OK;
@@ -297,7 +300,30 @@ int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const
     TRY(mark(1, st));
     TRY(launch_quant_rows(x, c.num_tokens, c.hidden_dim, w.xq, w.xs, st));
     TRY(mark(2, st));
-    return moe_experts(DT_FP8, c, w, w.xq, w.xs, w1, w1_scale, w2, w2_scale, y, st);
+    return moe_experts(DT_FP8, c, w, w.xq, w.xs, w1, w1_scale, w2, w2_scale, y, st, packed);
+}
+
+int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
+                           const float* w1_scale, const uint8_t* w2, const float* w2_scale,
+                           uint16_t* y, const MoeConfig* cfg, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    return forward_fp8(x, gate_weight, w1, w1_scale, w2, w2_scale, y, cfg, workspace,
+                       workspace_bytes, stream, false);
+}
+
+int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight,
+                                  const uint8_t* w1_packed, const float* w1_scale,
+                                  const uint8_t* w2_packed, const float* w2_scale, uint16_t* y,
+                                  const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    return forward_fp8(x, gate_weight, w1_packed, w1_scale, w2_packed, w2_scale, y, cfg, workspace,
+                       workspace_bytes, stream, true);
+}
+
+int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int cols, uint8_t* out,
+                            void* stream) {
+    AMDMOE_CHECK_ARG(w && out, "null tensor pointer");
+    return launch_pack_weights(w, num_experts, rows, cols, out, (hipStream_t)stream);
 }
 
 int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_indices,

@@ -21,6 +21,7 @@ struct GemmArgs {
     const uint8_t* b;        // expert weights base
     long b_expert_bytes;     // bytes per expert
     long b_row_bytes;        // bytes per weight row (K * element size)
+    int b_packed;            // weights in 16-row x 128-byte fragment blocks (pack_weights)
     const float* b_scale;    // fp8: [E][b_rows/128][K/128]
     int b_rows;              // weight rows per expert (2I or D)
     int K;                   // reduction length in elements
@@ -60,6 +61,10 @@ int launch_quant_weight(const float* w, long rows, int cols, const float* u, uin
 // moe_gemm.hip
 long max_mtiles(long P, int E);
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
+
+// moe_pack.hip: [E][N][K]-byte weights -> fragment-block order (N % 16 == 0,
+// K % 128 == 0)
+int launch_pack_weights(const uint8_t* w, long E, long N, long K, uint8_t* out, hipStream_t st);
 
 // moe_combine.hip
 int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,

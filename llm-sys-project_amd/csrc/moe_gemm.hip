@@ -197,7 +197,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             n = (long)nt * 256 + 32 * wave + 16 * ct + r16;
             ok = n < g.n_out;
         }
-        voff_b[ct] = ok ? (uint32_t)(n * g.b_row_bytes + 16 * q) : kOob;
+        // row-major: lane (q, r16) reads row n at K offset 16q (+64 for the
+        // hi half); fragment blocks: the 16 rows' 2 KB K-step is stored as
+        // [half][lane][16 B], so each load is 1 KB contiguous
+        const long nb = g.b_packed ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
+        voff_b[ct] = ok ? (uint32_t)nb : kOob;
     }
     if (DT == DT_FP8) {
         // weight scales of this work item for every K block -> LDS
@@ -248,8 +252,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const int kb = kblk(kt_b);
             const int ct = (sl - kASlots) >> 1;
             const uint32_t vo = live ? voff_b[ct] : kOob;
-            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<64>(rb, vo, kb * 128);
-            else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, kb * 128);
+            const int sstep = g.b_packed ? kb * 2048 : kb * 128;
+            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (g.b_packed ? 1024 : 64));
+            else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
         }
     };
 

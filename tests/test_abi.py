@@ -86,3 +86,16 @@ def test_workspace_too_small_is_reported():
                                     ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.byref(cfg),
                                     ctypes.c_void_p(4096), 16, None)
     assert rc == 3 and b"workspace" in lib.amdmoe_last_error()
+
+
+def test_pack_weights_validates_before_device_work():
+    lib = amdmoe.load()
+    p = ctypes.c_void_p(4096)
+    assert lib.amdmoe_pack_weights_fp8(None, 1, 16, 128, p, None) == 1
+    assert b"null" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_fp8(p, 1, 24, 128, ctypes.c_void_p(8192), None) == 1
+    assert b"16" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_fp8(p, 1, 16, 192, ctypes.c_void_p(8192), None) == 1
+    assert b"128" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_fp8(p, 1, 16, 128, p, None) == 1
+    assert b"in-place" in lib.amdmoe_last_error()

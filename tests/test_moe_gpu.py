@@ -351,3 +351,65 @@ def test_forward_fp8_dsv3_t4096_sampled(amd, orc, dsv3):
     announce("forward_fp8 dsv3 T=4096 sampled")
     rows = np.random.default_rng(4).choice(4096, 6, replace=False)
     assert _fp8_case(amd, orc, dsv3, 4096, 256, 8, 7168, 2048, sample=rows) < 2e-2
+
+
+# ------------------------------------------------------------------ packed weights
+def _pack_np(w):
+    """The fragment-block order of amdmoe_pack_weights_fp8 restated on the host:
+    block (e, n16, kb) holds, at [h][l][16 B], row 16*n16 + (l & 15), bytes
+    128*kb + 64*h + 16*(l >> 4) .. +15 of expert e."""
+    E, N, K = w.shape
+    b = w.reshape(E, N // 16, 16, K // 128, 2, 4, 16)  # e, n16, r, kb, h, q, byte
+    return np.ascontiguousarray(b.transpose(0, 1, 3, 4, 5, 2, 6)).reshape(E, N, K)
+
+
+def test_pack_weights_format(amd):
+    announce("pack_weights_fp8 format")
+    w = np.random.default_rng(11).integers(0, 256, size=(3, 48, 384), dtype=np.uint8)
+    out = torch.empty((3, 48, 384), dtype=torch.uint8, device="cuda")
+    amd.pack_weights_fp8(dev(w), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out), _pack_np(w))
+    # lane 17 of block (0, 0, 1), hi half = row 1, bytes 128 + 64 + 16 .. +15
+    assert np.array_equal(host(out)[0].reshape(-1)[1 * 2048 + 1024 + 17 * 16:][:16], w[0, 1, 208:224])
+
+
+def _packed_pair(w1q, w2q):
+    p1, p2 = torch.empty_like(w1q), torch.empty_like(w2q)
+    import amdmoe
+    amdmoe.pack_weights_fp8(w1q, p1)
+    amdmoe.pack_weights_fp8(w2q, p2)
+    return p1, p2
+
+
+def test_forward_fp8_packed_bit_identical_small(amd):
+    import synth
+    announce("forward_fp8_packed small")
+    T, E, K, D, I = 64, 16, 4, 512, 256
+    w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=78)
+    x, wg = synth.dsv3_inputs(T, E, D, seed=79)
+    p1, p2 = _packed_pair(w1q, w2q)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y0 = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    y1 = torch.empty_like(y0)
+    amd.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y0, cfg)
+    amd.moe_forward_fp8_packed(x, wg, p1, w1s, p2, w2s, y1, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+
+
+def test_forward_fp8_packed_bit_identical_dsv3_t4096(amd, dsv3):
+    import synth
+    announce("forward_fp8_packed dsv3 T=4096")
+    w1q, w1s, w2q, w2s = dsv3
+    T, E, K, D, I = 4096, 256, 8, 7168, 2048
+    x, wg = synth.dsv3_inputs(T, E, D, seed=1236)
+    p1, p2 = _packed_pair(w1q, w2q)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y0 = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    y1 = torch.empty_like(y0)
+    amd.moe_forward_fp8(x, wg, w1q, w1s, w2q, w2s, y0, cfg)
+    amd.moe_forward_fp8_packed(x, wg, p1, w1s, p2, w2s, y1, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    del p1, p2
