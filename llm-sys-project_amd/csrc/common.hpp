@@ -8,6 +8,9 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "../../include/amdmoe.h"
 
 namespace amdmoe {
@@ -142,6 +145,28 @@ __device__ __forceinline__ void bare_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// LDS writes issued before it are visible to every wave after it: waits for
+// this wave's LDS operations only (lgkmcnt(0); vector-memory and export
+// counters unconstrained, so direct-to-LDS loads keep flowing), then
+// s_barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order
+// (compile-time indices, e.g. for instruction immediates)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>());
 }
 
 // ------------------------------------------------------------------ host

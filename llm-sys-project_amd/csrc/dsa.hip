@@ -142,6 +142,24 @@ __device__ __forceinline__ float xor32_sum(float v) {
 }
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
+// Physical cache row of each of a query's S selected tokens -> LDS, by the
+// 256 threads of the block (paged latent cache: logical token i lives in
+// row page_table[i / page] * page + i % page).  All index loads are issued
+// before any page-table load, so the prologue costs two load latencies.
+template <int N>
+__device__ __forceinline__ void translate_rows(const int* __restrict__ lg, const int* __restrict__ pt,
+                                               int S, int page, int* s_rows) {
+    const int tid = threadIdx.x;
+    int li[N], pg[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) li[k] = tid + 256 * k < S ? lg[tid + 256 * k] : 0;
+#pragma unroll
+    for (int k = 0; k < N; k++) pg[k] = tid + 256 * k < S ? pt[li[k] / page] : 0;
+#pragma unroll
+    for (int k = 0; k < N; k++)
+        if (tid + 256 * k < S) s_rows[tid + 256 * k] = pg[k] * page + li[k] % page;
+}
+
 __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
     const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
@@ -165,10 +183,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     const int my_head = h0 + 16 * hg + c16;
 
     // page-table translation of this query's indices: physical row, or -1
-    for (int s = tid; s < S; s += 256) {
-        const int i = logical[(size_t)qi * S + s];
-        s_rows[s] = page_table[(size_t)qi * pages_per_seq + i / page] * page + i % page;
-    }
+    translate_rows<kMaxS / 256>(logical + (size_t)qi * S, page_table + (size_t)qi * pages_per_seq,
+                                S, page, s_rows);
 
     // q of my head as B fragments: 18 K-steps of 32 dims, group g holds 8
     u32x4 qf[18];
@@ -324,6 +340,250 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     }
 }
 
+// ------------------------------------------------------ 64-token tiles
+// dsa_bf16_paged64_kernel (S <= 2048): one workgroup per (query, 32
+// heads), 4 waves, 64-token tiles in a 2-stage LDS ring.  Every token row
+// is read from LDS once for S and once for V:
+//   wave w computes S^T for tokens 16w..16w+15 of the tile and all 32 heads
+//     (two MFMA column tiles; q of the 32 heads held in registers);
+//   the 4 waves share one running max per head (tile maxima exchanged
+//     through LDS) and write their P (bf16) to LDS;
+//   wave w then computes O^T += V^T . P^T for output dims 128w..128w+127
+//     over all 64 tokens (16x16x32 MFMA, K = 32 tokens, two K halves).
+// No merge is needed at the end: each wave owns a quarter of the output.
+// Tile layout in LDS (tile64_off): 1 KB blocks of 16 tokens x 4 chunks
+// (16-byte chunk j of the 1152-byte row), [token][chunk slot] with slot =
+// (j & 3) ^ ((token >> 2) & 3).  The DMA of wave w, instruction n, lane l
+// fills block (w, n) at 16 l, so the 4 lanes of a token read one 64-byte run
+// of its row (coalesced); a 16-token S^T fragment read (lane = token, one
+// chunk) and a transposed V^T read (4 tokens x 2 chunks per 16 lanes) both
+// hit distinct banks; all loop addresses are a base plus an immediate.
+constexpr int kT64 = 64;
+constexpr int kStage64 = kT64 * kRowBytes;                 // 73728
+constexpr int kMaxS64 = 2048;
+constexpr int kRows64Off = 2 * kStage64;                   // 147456
+constexpr int kP64Off = kRows64Off + kMaxS64 * 4;          // 155648
+constexpr int kMax64Off = kP64Off + 4 * 1024;              // 159744
+constexpr int kDsa64Lds = kMax64Off + 4 * 32 * 4;          // 160256
+
+__device__ __forceinline__ int tile64_off(int t, int j) {  // token t (0..63), chunk j (0..71)
+    return ((t >> 4) * 18 + (j >> 2)) * 1024 + (t & 15) * 64 + ((j & 3) ^ ((t >> 2) & 3)) * 16;
+}
+
+__global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
+    const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
+    const int* __restrict__ logical, uint16_t* __restrict__ out, int Q, int H, int S, int page,
+    int pages_per_seq, float scale_log2) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int* s_rows = (int*)(smem + kRows64Off);
+    uint16_t* s_p = (uint16_t*)(smem + kP64Off);    // [ht][head 16][token 64] bf16
+    float* s_max = (float*)(smem + kMax64Off);      // [wave][32 heads]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // XCD remap as in dsa_bf16_paged_kernel: a query's head groups share an XCD
+    const int nblk = gridDim.x, per = nblk / 8;
+    const int lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int hgroups = H / 32;
+    const int qi = lin / hgroups;
+    if (qi >= Q) return;
+    const int h0 = (lin % hgroups) * 32;
+    const int g = lane >> 4, c16 = lane & 15;
+
+    translate_rows<kMaxS64 / 256>(logical + (size_t)qi * S, page_table + (size_t)qi * pages_per_seq,
+                                  S, page, s_rows);
+    // q of heads h0 + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
+    u32x4 qf[2][18];
+#pragma unroll
+    for (int ht = 0; ht < 2; ht++) {
+        const size_t hrow = (size_t)qi * H + h0 + 16 * ht + c16;
+        const uint16_t* qnr = qn + hrow * kDc;
+        const uint16_t* qpr = qp + hrow * kDp;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qf[ht][ks] = *(const u32x4*)(qnr + 32 * ks + 8 * g);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) qf[ht][16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
+    }
+    __syncthreads();  // s_rows visible; regular loads complete
+
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
+    // DMA lane l: token 16w + (l >> 2), chunk 4n + ((l & 3) ^ ((l >> 4) & 3))
+    const int my_tok = 16 * wave + (lane >> 2);
+    const int my_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    // Tile loads: 18 per wave, one per 64-byte chunk group n.  The row
+    // offset of group n goes in soffset: an instruction immediate would also
+    // shift the LDS destination.
+    auto tile_vo = [&](int tile) {
+        const int tok = tile * kT64 + my_tok;
+        return tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * my_chunk) : kOob;
+    };
+    auto issue_n = [&](int st, uint32_t vo, int n) __attribute__((always_inline)) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rc, (lds_ptr_t)(smem + st * kStage64 + wave * 18 * 1024 + n * 1024), 16, vo, 64 * n, 0, 0);
+    };
+
+    f32x4 o[8][2];  // dims 128w + 16mt + 4g + i, head c16 of tile ht
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        for (int j = 0; j < 2; j++) o[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    const int ntiles = (S + kT64 - 1) / kT64;
+
+    // V^T transposed reads: K half kh (tokens 32kh..), group g of 8 tokens,
+    // half r: lane (g, s) supplies token 32kh + 8g + 4r + (s >> 2), dims
+    // d0 + 4(s & 3) .. +3; dim tile mt sits at voff[kh][r][mt & 1] + 1024 (mt >> 1)
+    int voff[2][2][2];
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int d = 128 * wave + 16 * e + 4 * (c16 & 3);
+                voff[kh][r][e] = tile64_off(32 * kh + 8 * g + 4 * r + (c16 >> 2), d >> 3) + (d & 7) * 2;
+            }
+    const int koff = tile64_off(16 * wave + c16, g);  // S^T fragment of K-step ks: + 1024 ks
+
+    {
+        const uint32_t vo0 = tile_vo(0);
+#pragma unroll
+        for (int n = 0; n < 18; n++) issue_n(0, vo0, n);
+    }
+    for (int t = 0; t < ntiles; t++) {
+        // the next tile's loads are spread over this tile's S^T steps (one
+        // per K-step) instead of issued in one burst
+        const bool more = t + 1 < ntiles;
+        const uint32_t vo_next = tile_vo(more ? t + 1 : t);
+        wait_vmcnt<0>();
+        bare_barrier();  // tile t landed everywhere; stage (t+1)&1 is free
+        const uint8_t* kb = smem + (t & 1) * kStage64;
+
+        // S^T for tokens 16w + (0..15), heads h0 + 16ht + (0..15): four
+        // accumulation chains (head tile x even/odd K-step)
+        f32x4 sacc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            for (int j = 0; j < 2; j++) sacc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        {
+            const uint8_t* krow = kb + koff;
+            // 10 fragment reads in flight: with one wave per SIMD the LDS
+            // only streams at full rate with many reads outstanding
+            constexpr int kPre = 10;
+            u32x4 a[18];
+#pragma unroll
+            for (int ks = 0; ks < kPre; ks++) a[ks] = *(const u32x4*)(krow + ks * 1024);
+#pragma unroll
+            for (int ks = 0; ks < 18; ks++) {
+                if (ks + kPre < 18) a[ks + kPre] = *(const u32x4*)(krow + (ks + kPre) * 1024);
+                sacc[0][ks & 1] = mfma_bf16(a[ks], qf[0][ks], sacc[0][ks & 1]);
+                sacc[1][ks & 1] = mfma_bf16(a[ks], qf[1][ks], sacc[1][ks & 1]);
+                if (more) issue_n((t + 1) & 1, vo_next, ks);
+            }
+        }
+        float sv[2][4], tm[2];
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++) {
+            tm[ht] = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tk = t * kT64 + 16 * wave + 4 * g + i;
+                sv[ht][i] = tk < S ? (sacc[ht][0][i] + sacc[ht][1][i]) * scale_log2 : -INFINITY;
+                tm[ht] = fmaxf(tm[ht], sv[ht][i]);
+            }
+            tm[ht] = xor32_max(xor16_max(tm[ht]));
+        }
+        if (g == 0) {
+            s_max[wave * 32 + c16] = tm[0];
+            s_max[wave * 32 + 16 + c16] = tm[1];
+        }
+        lds_barrier();
+        // the tile max over all 64 tokens; the running max is raised only
+        // when it grows by more than 8 (p <= 256 in bf16), so the O rescale
+        // is rare.  Every wave reads the same values: the same decision.
+        bool raise = false;
+        float mt4[2];
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++) {
+            mt4[ht] = fmaxf(fmaxf(s_max[16 * ht + c16], s_max[32 + 16 * ht + c16]),
+                            fmaxf(s_max[64 + 16 * ht + c16], s_max[96 + 16 * ht + c16]));
+            raise |= mt4[ht] > m_run[ht] + 8.0f;
+        }
+        if (__ballot(raise)) {
+#pragma unroll
+            for (int ht = 0; ht < 2; ht++) {
+                const float m_new = fmaxf(m_run[ht], mt4[ht]);
+                const float corr = m_run[ht] == -INFINITY ? 0.0f : exp2f(m_run[ht] - m_new);
+                l_run[ht] *= corr;
+#pragma unroll
+                for (int mt = 0; mt < 8; mt++) o[mt][ht] *= corr;
+                m_run[ht] = m_new;
+            }
+        }
+        // P (bf16), head-major [ht][c16][token 0..63]; l over this wave's tokens
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++) {
+            float pv[4], psum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pv[i] = sv[ht][i] == -INFINITY ? 0.0f : exp2f(sv[ht][i] - m_run[ht]);
+                psum += pv[i];
+            }
+            l_run[ht] += xor32_sum(xor16_sum(psum));
+            const u32x2 pk = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+            *(u32x2*)(s_p + (ht * 16 + c16) * 64 + 16 * wave + 4 * g) = pk;
+        }
+        lds_barrier();
+        // O^T (dims 128w + 16mt + 4g + i, head c16) += V^T . P^T over 64 tokens
+        u32x4 pb[2][2];  // [K half][ht]
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int ht = 0; ht < 2; ht++)
+                pb[kh][ht] = *(const u32x4*)(s_p + (ht * 16 + c16) * 64 + 32 * kh + 8 * g);
+        auto vfrag = [&](int i) __attribute__((always_inline)) {  // i = 2 mt + kh
+            const int mt = i >> 1, kh = i & 1;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_ptr)(kb + voff[kh][0][mt & 1] + 1024 * (mt >> 1)));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_ptr)(kb + voff[kh][1][mt & 1] + 1024 * (mt >> 1)));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+            return (u32x4){l2[0], l2[1], h2[0], h2[1]};
+        };
+        constexpr int kPreV = 6;
+        u32x4 va[16];
+#pragma unroll
+        for (int i = 0; i < kPreV; i++) va[i] = vfrag(i);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            if (i + kPreV < 16) va[i + kPreV] = vfrag(i + kPreV);
+            const int mt = i >> 1, kh = i & 1;
+            o[mt][0] = mfma_bf16(va[i], pb[kh][0], o[mt][0]);
+            o[mt][1] = mfma_bf16(va[i], pb[kh][1], o[mt][1]);
+        }
+    }
+    __syncthreads();  // every wave is done with s_p / s_max
+
+    // l over all 64 tokens of each tile: sum of the 4 waves' shares
+    float* xs = (float*)smem;                          // ring no longer read
+#pragma unroll
+    for (int ht = 0; ht < 2; ht++) xs[(wave * 2 + ht) * 64 + lane] = l_run[ht];
+    __syncthreads();
+#pragma unroll
+    for (int ht = 0; ht < 2; ht++) {
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) l += xs[(w * 2 + ht) * 64 + lane];
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        uint16_t* orow = out + ((size_t)qi * H + h0 + 16 * ht + c16) * kDc + 128 * wave;
+#pragma unroll
+        for (int mt = 0; mt < 8; mt++) {
+            const u32x2 pk = {pack_bf16x2(o[mt][ht][0] * inv, o[mt][ht][1] * inv),
+                              pack_bf16x2(o[mt][ht][2] * inv, o[mt][ht][3] * inv)};
+            *(u32x2*)(orow + 16 * mt + 4 * g) = pk;
+        }
+    }
+}
+
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
                           long cache_tokens, const int* page_table, const int* logical,
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
@@ -346,6 +606,19 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
     const int nblk = Q * (H / 32);
     const int grid = (nblk + 7) / 8 * 8;
     const float scale_log2 = 1.0f / sqrtf((float)(Dc + Dp)) * 1.4426950408889634f;
+    if (S <= kMaxS64) {
+        static bool attr64_set = false;
+        if (!attr64_set) {
+            AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_bf16_paged64_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDsa64Lds));
+            attr64_set = true;
+        }
+        hipLaunchKernelGGL(dsa_bf16_paged64_kernel, dim3(grid), dim3(256), kDsa64Lds, st, qn, qp,
+                           cache, cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,
+                           pages_per_seq, scale_log2);
+        AMDMOE_LAUNCH_CHECK();
+        return AMDMOE_OK;
+    }
     hipLaunchKernelGGL(dsa_bf16_paged_kernel, dim3(grid), dim3(256), kDsaLds, st, qn, qp, cache,
                        cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,
                        pages_per_seq, scale_log2);

@@ -67,16 +67,6 @@ template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
 template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
 template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
 
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>()), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>());
-}
-
 // One K-step of a wave's weights in registers: per column tile the lane's
 // 32 bytes, lo 16 B at K offset 16q and hi 16 B at 64 + 16q (the fp8 MFMA
 // consumes them as one 8-dword tuple).
