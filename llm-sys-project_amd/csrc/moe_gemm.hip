@@ -58,7 +58,8 @@ constexpr int kBScaleOff = kNS * kStageBytes;          // fp8 weight scales [2][
 constexpr int kMaxKb = 128;                            // K <= 16384 on the fp8 path
 constexpr int kEpiPitch = 132;                         // floats per staged output row
 constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
-constexpr int kGemmLds = kBScaleOff + 2 * kMaxKb * 4;  // 105472
+constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
+constexpr int kGemmLds = kRowInfoOff + kBM * 8;           // 107520
 static_assert(kEpiRows * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
 static_assert(kBM == 256, "the wave layout assumes 256-row tiles");
 
@@ -193,6 +194,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         const long nb = g.b_packed ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
         voff_b[ct] = ok ? (uint32_t)nb : kOob;
     }
+    // DOWN: the flat slot and routing weight of each of the tile's rows ->
+    // LDS (two dependent gathers, overlapped with the scale loads below and
+    // waited for by the barrier before the main loop)
+    int row_slot = 0;
+    if (MODE == MODE_DOWN && tid < rows) row_slot = g.sorted_slot[(size_t)row0 + tid];
     if (DT == DT_FP8) {
         // weight scales of this work item for every K block -> LDS
         float* sbs = (float*)(smem + kBScaleOff);
@@ -203,6 +209,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                                            : min(2 * nt + which, g.b_rows / 128 - 1);
             sbs[which * kMaxKb + kb] = bse[(size_t)nb * kb_per_row + kb];
         }
+    }
+    if (MODE == MODE_DOWN && tid < kBM) {
+        ((int*)(smem + kRowInfoOff))[tid] = row_slot;
+        ((float*)(smem + kRowInfoOff))[kBM + tid] = tid < rows ? g.wts[row_slot] : 0.0f;
     }
 
     // K-steps run in a rotated order starting at kt0, keyed by the M-tile:
@@ -481,7 +491,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 f32x4 hv;
                 for (int i = 0; i < 4; i++) {
                     const float gv = acc[rt][0][i], uv = acc[rt][1][i];
-                    const float silu = gv / (1.0f + expf(-gv));
+                    // fp32 keeps the reference's expf and IEEE division
+                    // (naive_moe.cu:297-310); the bf16 / fp8 epilogues use
+                    // the hardware exp2 and reciprocal (~1 ulp each)
+                    const float silu = DT == DT_F32 ? gv / (1.0f + expf(-gv))
+                                                    : gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
                     hv[i] = silu * uv;
                 }
                 *(f32x4*)&Tb[(16 * r8 + r16) * kEpiPitch + 16 * wave + 4 * q] = hv;
@@ -499,13 +513,17 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
                 amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
                 const float s = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 1.0f;
+                // q = v * (1/s): one correctly rounded reciprocal per block
+                // instead of 32 divisions (codes may differ from v / s by one
+                // step where v / s lies within an ulp of an e4m3 midpoint)
+                const float inv = __fdiv_rn(1.0f, s);
                 if (ok) {
                     u32x4 o0, o1;
                     for (int k = 0; k < 4; k++) {
-                        o0[k] = f32x4_to_e4m3x4(__fdiv_rn(v[4 * k], s), __fdiv_rn(v[4 * k + 1], s),
-                                                __fdiv_rn(v[4 * k + 2], s), __fdiv_rn(v[4 * k + 3], s));
-                        o1[k] = f32x4_to_e4m3x4(__fdiv_rn(v[16 + 4 * k], s), __fdiv_rn(v[16 + 4 * k + 1], s),
-                                                __fdiv_rn(v[16 + 4 * k + 2], s), __fdiv_rn(v[16 + 4 * k + 3], s));
+                        o0[k] = f32x4_to_e4m3x4(v[4 * k] * inv, v[4 * k + 1] * inv,
+                                                v[4 * k + 2] * inv, v[4 * k + 3] * inv);
+                        o1[k] = f32x4_to_e4m3x4(v[16 + 4 * k] * inv, v[16 + 4 * k + 1] * inv,
+                                                v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
                     }
                     uint8_t* dst = g.out + pos * g.n_out + col;
                     *(u32x4*)dst = o0;
@@ -530,46 +548,29 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
         }
     } else {
-        // 256 output columns = 2 passes of 128 (waves 4h..4h+3 own pass h),
-        // each over up to 2 halves of 128 rows
-        bool first = true;
+        // Stored straight from the accumulators: lane (q, r16) holds output
+        // columns n0 + 4q .. +3 of token row 16 rt + r16, so each row's 512
+        // bytes are written as 8-byte (bf16) or 16-byte (fp32) pieces; the
+        // row's slot and routing weight come from LDS.
+        const int* s_slot = (const int*)(smem + kRowInfoOff);
+        const float* s_wt = (const float*)(smem + kRowInfoOff) + kBM;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int rt = 0; rt < 16; rt++) {
+            if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
+            const int r = 16 * rt + r16;
+            if (r >= rows) continue;
+            const size_t sl = (size_t)s_slot[r];
+            const float wgt = s_wt[r];
 #pragma unroll
-            for (int half = 0; half < 2; half++) {
-                if (128 * half >= rows) continue;
-                if (!first) __syncthreads();
-                first = false;
-                if ((wave >> 2) == h) {
-#pragma unroll
-                    for (int r8 = 0; r8 < 8; r8++) {
-                        const int rt = 8 * half + r8;
-                        for (int ct = 0; ct < 2; ct++)
-                            *(f32x4*)&Tb[(16 * r8 + r16) * kEpiPitch + 32 * (wave & 3) + 16 * ct + 4 * q] =
-                                acc[rt][ct];
-                    }
-                }
-                __syncthreads();
-                const int rr = 128 * half + er;
-                const int n = nt * 256 + 128 * h + 32 * pp;
-                if (rr < rows && n < g.n_out) {
-                    const size_t pos = (size_t)row0 + rr;
-                    const int sl = g.sorted_slot[pos];
-                    const float wgt = g.wts[sl];
-                    float v[32];
-                    for (int j = 0; j < 32; j++) v[j] = wgt * Tb[er * kEpiPitch + 32 * pp + j];
-                    if (DT == DT_F32) {
-                        float* dst = (float*)g.out + (size_t)sl * g.n_out + n;
-                        for (int k = 0; k < 8; k++)
-                            *(f32x4*)(dst + 4 * k) = (f32x4){v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
-                    } else {
-                        uint8_t* dst = g.out + ((size_t)sl * g.n_out + n) * 2;
-                        for (int k = 0; k < 4; k++) {
-                            u32x4 o;
-                            for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(v[8 * k + 2 * m], v[8 * k + 2 * m + 1]);
-                            *(u32x4*)(dst + 16 * k) = o;
-                        }
-                    }
+            for (int ct = 0; ct < 2; ct++) {
+                const int n = nt * 256 + 32 * wave + 16 * ct + 4 * q;
+                if (n >= g.n_out) continue;
+                const f32x4 v = acc[rt][ct] * wgt;
+                if (DT == DT_F32) {
+                    *(f32x4*)((float*)g.out + sl * g.n_out + n) = v;
+                } else {
+                    const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    *(u32x2*)(g.out + (sl * g.n_out + n) * 2) = pk;
                 }
             }
         }
