@@ -49,6 +49,7 @@ struct MoeWs {
     float* act_s;
     uint8_t* ypair;
     float* logits;  // gate logits scratch of the MFMA routing (fp8 path)
+    int* perm;      // permutation scratch (per-block counts and offsets)
     size_t total;
 };
 
@@ -74,6 +75,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     w.tiles = (int4*)take(16 * (size_t)max_mtiles((long)P, (int)E));
     w.sorted_token = (int*)take(4 * P);
     w.sorted_slot = (int*)take(4 * P);
+    w.perm = (int*)take(permute_scratch_bytes((int)T, (int)E));
     if (dtype == AMDMOE_DTYPE_FP8) {
         w.xq = take(T * D);
         w.xs = (float*)take(4 * T * (D / 128));
@@ -164,7 +166,8 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     const long mtiles = max_mtiles(P, E);
     const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);
     TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
-                       w.sorted_slot, w.tiles, w.num_tiles, st));
+                       w.sorted_slot, w.tiles, w.num_tiles,
+                       permute_scratch_bytes(T, E) ? w.perm : nullptr, st));
     TRY(mark(3, st));
     GemmArgs up{};
     up.a = a_x;
@@ -383,12 +386,15 @@ int amdmoe_moe_permute(const int* expert_indices, const MoeConfig* cfg, int* cou
     // the tile table is not part of this entry's outputs: a private buffer
     // of the cached workspace holds it
     const long mt = max_mtiles((long)c.num_tokens * c.top_k, c.num_experts);
+    const size_t tiles_bytes = align_up(16 * (size_t)(mt + 1), 256);
+    const size_t perm_bytes = permute_scratch_bytes(c.num_tokens, c.num_experts);
     void* scratch = nullptr;
-    TRY(cached_workspace(align_up(16 * (size_t)(mt + 1), 256) + 256, &scratch));
+    TRY(cached_workspace(tiles_bytes + 256 + perm_bytes, &scratch));
     int4* tiles = (int4*)scratch;
-    int* nt = (int*)((uint8_t*)scratch + align_up(16 * (size_t)(mt + 1), 256));
+    int* nt = (int*)((uint8_t*)scratch + tiles_bytes);
+    int* perm = perm_bytes ? (int*)((uint8_t*)scratch + tiles_bytes + 256) : nullptr;
     return launch_permute(expert_indices, c.num_tokens, c.top_k, c.num_experts, kMTile, counts,
-                          offsets, sorted_token, sorted_slot, tiles, nt, (hipStream_t)stream);
+                          offsets, sorted_token, sorted_slot, tiles, nt, perm, (hipStream_t)stream);
 }
 
 int amdmoe_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,

@@ -46,9 +46,12 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
                       float* wts, float* logits, hipStream_t st);
 
 // moe_permute.hip
+// scratch: permute_scratch_bytes(T, E) bytes, or nullptr (single-launch
+// kernel); permute_scratch_bytes returns 0 where only the latter applies
+size_t permute_scratch_bytes(int T, int E);
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   hipStream_t st);
+                   int* scratch, hipStream_t st);
 int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D, int expert,
                       float* gathered, int* token_map, int* count, hipStream_t st);
 

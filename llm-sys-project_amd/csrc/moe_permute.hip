@@ -136,9 +136,156 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     }
 }
 
+// ------------------------------------------------- three-launch variant
+// For E <= 1024 with a scratch of 2 * ceil(T/64) * E ints.  Blocks of 64
+// tokens (one wave, lane = token):
+//   perm_count_kernel: per block, a 64-bit lane mask per expert in LDS
+//     (bit l: token 64b+l lists the expert, first occurrence only);
+//     blk_cnt[b][e] = popcount(mask[e]);
+//   perm_scan_kernel (one block): per expert, exclusive offsets over blocks
+//     and the expert's row / M-tile offsets; counts, offsets, tile table;
+//   perm_scatter_kernel: rebuilds the masks; token 64b+l goes to row
+//     blk_off[b][e] + popcount(mask[e] & lanes below l).
+// Rows of an expert are thus in ascending token order (block, then lane):
+// the same order as the single-launch kernel above.
+constexpr int kPermTok = 64;
+
+__device__ __forceinline__ void perm_masks(const int* __restrict__ idx, int T, int K, int E,
+                                           unsigned long long* s_mask) {
+    const int lane = threadIdx.x;
+    for (int e = lane; e < E; e += kPermTok) s_mask[e] = 0ull;
+    __syncthreads();
+    const int t = blockIdx.x * kPermTok + lane;
+    if (t < T) {
+        const int* row = idx + (size_t)t * K;
+        for (int k = 0; k < K; k++) {
+            const int v = row[k];
+            if (v < 0 || v >= E) continue;
+            bool dup = false;
+            for (int j = 0; j < k; j++) dup |= row[j] == v;
+            if (!dup) atomicOr(&s_mask[v], 1ull << lane);
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kPermTok) void perm_count_kernel(const int* __restrict__ idx, int T,
+                                                              int K, int E, int* __restrict__ blk_cnt) {
+    extern __shared__ unsigned long long s_mask[];  // [E]
+    perm_masks(idx, T, K, E, s_mask);
+    for (int e = threadIdx.x; e < E; e += kPermTok)
+        blk_cnt[(size_t)blockIdx.x * E + e] = __popcll(s_mask[e]);
+}
+
+__global__ __launch_bounds__(1024) void perm_scan_kernel(const int* __restrict__ blk_cnt,
+                                                         int* __restrict__ blk_off, int nblk, int E,
+                                                         int BM, int* __restrict__ counts,
+                                                         int* __restrict__ offsets,
+                                                         int4* __restrict__ tiles,
+                                                         int* __restrict__ num_tiles) {
+    // thread (p, e): expert e, block range p of NP = 1024 / Ep ranges, so the
+    // per-block counts of an expert are read by NP threads in parallel
+    __shared__ int s_part[1024], s_rows[1024], s_tiles[1024];
+    int Ep = 1;
+    while (Ep < E) Ep <<= 1;
+    const int NP = 1024 / Ep;
+    const int e = threadIdx.x % Ep, p = threadIdx.x / Ep;
+    const int chunk = (nblk + NP - 1) / NP;
+    const int b0 = p * chunk, b1 = min(nblk, b0 + chunk);
+    int part = 0;
+    if (e < E)
+        for (int b = b0; b < b1; b++) part += blk_cnt[(size_t)b * E + e];
+    s_part[threadIdx.x] = part;
+    __syncthreads();
+    int before = 0, tot = 0;
+    for (int pp = 0; pp < NP; pp++) {
+        const int v = s_part[pp * Ep + e];
+        if (pp < p) before += v;
+        tot += v;
+    }
+    const int nt = (tot + BM - 1) / BM;
+    if (p == 0) {
+        s_rows[e] = e < E ? tot : 0;
+        s_tiles[e] = e < E ? nt : 0;
+    }
+    __syncthreads();
+    // inclusive scans over experts (Hillis-Steele over Ep entries)
+    for (int o = 1; o < Ep; o <<= 1) {
+        int r = 0, tl = 0;
+        if (p == 0 && e >= o) { r = s_rows[e - o]; tl = s_tiles[e - o]; }
+        __syncthreads();
+        if (p == 0) { s_rows[e] += r; s_tiles[e] += tl; }
+        __syncthreads();
+    }
+    if (e < E) {
+        const int row_off = s_rows[e] - tot;
+        int run = row_off + before;
+        for (int b = b0; b < b1; b++) {
+            blk_off[(size_t)b * E + e] = run;
+            run += blk_cnt[(size_t)b * E + e];
+        }
+        if (p == 0) {
+            const int tile_off = s_tiles[e] - nt;
+            counts[e] = tot;
+            offsets[e] = row_off;
+            for (int j = 0; j < nt; j++)
+                tiles[tile_off + j] = make_int4(e, row_off + j * BM, min(BM, tot - j * BM), 0);
+            if (e == E - 1) {
+                offsets[E] = s_rows[e];
+                *num_tiles = s_tiles[e];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int* __restrict__ idx, int T,
+                                                                int K, int E,
+                                                                const int* __restrict__ blk_off,
+                                                                int* __restrict__ sorted_token,
+                                                                int* __restrict__ sorted_slot) {
+    extern __shared__ unsigned long long s_mask[];  // [E]
+    perm_masks(idx, T, K, E, s_mask);
+    const int lane = threadIdx.x;
+    const int t = blockIdx.x * kPermTok + lane;
+    if (t >= T) return;
+    const int* row = idx + (size_t)t * K;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int k = 0; k < K; k++) {
+        const int v = row[k];
+        if (v < 0 || v >= E) continue;
+        bool dup = false;
+        for (int j = 0; j < k; j++) dup |= row[j] == v;
+        if (dup) continue;
+        const int pos = blk_off[(size_t)blockIdx.x * E + v] + __popcll(s_mask[v] & below);
+        sorted_token[pos] = t;
+        sorted_slot[pos] = t * K + k;
+    }
+}
+
+size_t permute_scratch_bytes(int T, int E) {
+    const long nblk = (T + kPermTok - 1) / kPermTok;
+    if (E > 1024 || nblk * E > (1L << 22)) return 0;
+    return (size_t)(2 * nblk * E) * sizeof(int);
+}
+
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   hipStream_t st) {
+                   int* scratch, hipStream_t st) {
+    if (scratch && T > 0 && permute_scratch_bytes(T, E) > 0) {
+        const int nblk = (T + kPermTok - 1) / kPermTok;
+        int* blk_cnt = scratch;
+        int* blk_off = scratch + (size_t)nblk * E;
+        const size_t lds = sizeof(unsigned long long) * (size_t)E;
+        hipLaunchKernelGGL(perm_count_kernel, dim3(nblk), dim3(kPermTok), lds, st, idx, T, K, E, blk_cnt);
+        AMDMOE_LAUNCH_CHECK();
+        hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(1024), 0, st, blk_cnt, blk_off, nblk, E, BM,
+                           counts, offsets, tiles, num_tiles);
+        AMDMOE_LAUNCH_CHECK();
+        hipLaunchKernelGGL(perm_scatter_kernel, dim3(nblk), dim3(kPermTok), lds, st, idx, T, K, E,
+                           blk_off, sorted_token, sorted_slot);
+        AMDMOE_LAUNCH_CHECK();
+        return AMDMOE_OK;
+    }
     size_t lds = sizeof(int) * (size_t)E;
     AMDMOE_CHECK_ARG(lds <= 48 * 1024, "permute: E=%d too large", E);
     hipLaunchKernelGGL(permute_kernel, dim3(E), dim3(kPermThreads), lds, st, idx, T, K, E, BM,

@@ -156,7 +156,10 @@ def test_gate_bias_and_bf16x(amd, orc):
 
 
 # ------------------------------------------------------------------ permutation
-@pytest.mark.parametrize("T,E,K", [(1, 4, 2), (4, 16, 2), (512, 8, 2), (4096, 256, 8), (300, 3, 5)])
+# (70, 2048, 4): E > 1024 takes the single-launch kernel; the others the
+# three-launch one (incl. a partial last block of 64 tokens and K > E)
+@pytest.mark.parametrize("T,E,K", [(1, 4, 2), (4, 16, 2), (512, 8, 2), (4096, 256, 8), (300, 3, 5),
+                                   (8192, 256, 8), (70, 2048, 4)])
 def test_permute_bit_exact(amd, orc, T, E, K):
     announce(f"permute T={T} E={E} K={K}")
     rng = np.random.default_rng(T + E)
