@@ -217,6 +217,45 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const int* logical_indices, uint16_t* output,
                                  const DsaConfig* cfg, int pages_per_seq, void* stream);
 
+/* The reference's DSA stage functions (fp32), same semantics; dsa_forward
+ * above does not go through them.  Shapes follow cfg: gathered_kc/v
+ * [Q,S,Dc], gathered_kp [Q,S,Dp], scores/attn [Q,H,S], output [Q,H,Dc].
+ * Every value is formed in the reference kernel's order (sequential fp32
+ * sums, no contraction). */
+
+/* Replaces dsa_kv_gather (naive_dsa.cuh:31-36, naive_dsa.cu:336-367):
+ * gathered_*[q,s,:] = cache row sparse_indices[q,s].  An index outside
+ * [0, cfg->total_kv_tokens) gathers a row of zeros. */
+int amdmoe_dsa_kv_gather_f32(const float* kv_cache_compressed, const float* kv_cache_positional,
+                             const float* v_cache, const int* sparse_indices, float* gathered_kc,
+                             float* gathered_kp, float* gathered_v, const DsaConfig* cfg,
+                             void* stream);
+
+/* Replaces dsa_dot_compressed (naive_dsa.cuh:42-43, naive_dsa.cu:89-134,
+ * 369-380): scores[q,h,s] += dot(q_nope[q,h,:], kc[q,s,:]). */
+int amdmoe_dsa_dot_compressed_f32(const float* q_nope, const float* kc, float* scores,
+                                  const DsaConfig* cfg, void* stream);
+
+/* Replaces dsa_dot_positional (naive_dsa.cuh:49-50, naive_dsa.cu:157-206,
+ * 382-393): scores[q,h,s] += dot(q_pe[q,h,:], kp[q,s,:]). */
+int amdmoe_dsa_dot_positional_f32(const float* q_pe, const float* kp, float* scores,
+                                  const DsaConfig* cfg, void* stream);
+
+/* Replaces dsa_dot_fused (naive_dsa.cuh:54-57, naive_dsa.cu:208-276,
+ * 395-409): scores[q,h,s] += dot over the concatenation [q_nope|q_pe] .
+ * [kc|kp], one accumulator. */
+int amdmoe_dsa_dot_fused_f32(const float* q_nope, const float* q_pe, const float* kc,
+                             const float* kp, float* scores, const DsaConfig* cfg, void* stream);
+
+/* Replaces dsa_softmax (naive_dsa.cuh:61, naive_dsa.cu:278-296, 411-418):
+ * per (q,h) row, in place: e = expf(x - max), x = e * (1/sum e). */
+int amdmoe_dsa_softmax_f32(float* scores, const DsaConfig* cfg, void* stream);
+
+/* Replaces dsa_output_proj (naive_dsa.cuh:67-68, naive_dsa.cu:300-316,
+ * 420-429): output[q,h,d] = sum_s attn[q,h,s] * v[q,s,d] (overwritten). */
+int amdmoe_dsa_output_proj_f32(const float* attn, const float* v, float* output,
+                               const DsaConfig* cfg, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,7 +23,9 @@ SYMBOLS = [
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
     "amdmoe_quant_weight_fp8", "amdmoe_set_stage_events", "amdmoe_dsa_forward_f32",
-    "amdmoe_dsa_decode_bf16_paged",
+    "amdmoe_dsa_decode_bf16_paged", "amdmoe_dsa_kv_gather_f32", "amdmoe_dsa_dot_compressed_f32",
+    "amdmoe_dsa_dot_positional_f32", "amdmoe_dsa_dot_fused_f32", "amdmoe_dsa_softmax_f32",
+    "amdmoe_dsa_output_proj_f32",
 ]
 
 
@@ -83,6 +85,12 @@ def load():
         "amdmoe_set_stage_events": (I, [ctypes.POINTER(_P)]),
         "amdmoe_dsa_forward_f32": (I, [_P, _P, _P, _P, _P, _P, _P, dcfgp, _P]),
         "amdmoe_dsa_decode_bf16_paged": (I, [_P, _P, _P, _P, _P, _P, dcfgp, I, _P]),
+        "amdmoe_dsa_kv_gather_f32": (I, [_P, _P, _P, _P, _P, _P, _P, dcfgp, _P]),
+        "amdmoe_dsa_dot_compressed_f32": (I, [_P, _P, _P, dcfgp, _P]),
+        "amdmoe_dsa_dot_positional_f32": (I, [_P, _P, _P, dcfgp, _P]),
+        "amdmoe_dsa_dot_fused_f32": (I, [_P, _P, _P, _P, _P, dcfgp, _P]),
+        "amdmoe_dsa_softmax_f32": (I, [_P, dcfgp, _P]),
+        "amdmoe_dsa_output_proj_f32": (I, [_P, _P, _P, dcfgp, _P]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -252,3 +260,33 @@ def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, out, cfg, pages_pe
     _check(load().amdmoe_dsa_decode_bf16_paged(_ptr(qn), _ptr(qp), _ptr(cache), _ptr(page_table),
                                                _ptr(logical), _ptr(out), ctypes.byref(cfg),
                                                pages_per_seq, _stream(stream)))
+
+
+# the reference's DSA stage functions (naive_dsa.cuh:31-68)
+def dsa_kv_gather_f32(kc, kp, v, idx, gkc, gkp, gv, cfg, stream=None):
+    _check(load().amdmoe_dsa_kv_gather_f32(_ptr(kc), _ptr(kp), _ptr(v), _ptr(idx), _ptr(gkc),
+                                           _ptr(gkp), _ptr(gv), ctypes.byref(cfg), _stream(stream)))
+
+
+def dsa_dot_compressed_f32(qn, kc, scores, cfg, stream=None):
+    _check(load().amdmoe_dsa_dot_compressed_f32(_ptr(qn), _ptr(kc), _ptr(scores),
+                                                ctypes.byref(cfg), _stream(stream)))
+
+
+def dsa_dot_positional_f32(qp, kp, scores, cfg, stream=None):
+    _check(load().amdmoe_dsa_dot_positional_f32(_ptr(qp), _ptr(kp), _ptr(scores),
+                                                ctypes.byref(cfg), _stream(stream)))
+
+
+def dsa_dot_fused_f32(qn, qp, kc, kp, scores, cfg, stream=None):
+    _check(load().amdmoe_dsa_dot_fused_f32(_ptr(qn), _ptr(qp), _ptr(kc), _ptr(kp), _ptr(scores),
+                                           ctypes.byref(cfg), _stream(stream)))
+
+
+def dsa_softmax_f32(scores, cfg, stream=None):
+    _check(load().amdmoe_dsa_softmax_f32(_ptr(scores), ctypes.byref(cfg), _stream(stream)))
+
+
+def dsa_output_proj_f32(attn, v, out, cfg, stream=None):
+    _check(load().amdmoe_dsa_output_proj_f32(_ptr(attn), _ptr(v), _ptr(out), ctypes.byref(cfg),
+                                             _stream(stream)))

@@ -442,6 +442,67 @@ int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* 
                           c.total_kv_tokens, (hipStream_t)stream);
 }
 
+static int dsa_cfg_check(const DsaConfig* cfg) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    const DsaConfig& c = *cfg;
+    AMDMOE_CHECK_ARG(c.num_queries >= 0 && c.num_heads >= 0 && c.head_dim_compressed >= 0 &&
+                         c.head_dim_positional >= 0 && c.num_selected_kv >= 0 &&
+                         c.total_kv_tokens >= 0,
+                     "bad DsaConfig");
+    return AMDMOE_OK;
+}
+
+int amdmoe_dsa_kv_gather_f32(const float* kv_cache_compressed, const float* kv_cache_positional,
+                             const float* v_cache, const int* sparse_indices, float* gathered_kc,
+                             float* gathered_kp, float* gathered_v, const DsaConfig* cfg,
+                             void* stream) {
+    TRY(dsa_cfg_check(cfg));
+    const DsaConfig& c = *cfg;
+    return launch_dsa_gather(kv_cache_compressed, kv_cache_positional, v_cache, sparse_indices,
+                             gathered_kc, gathered_kp, gathered_v, c.num_queries,
+                             c.num_selected_kv, c.head_dim_compressed, c.head_dim_positional,
+                             c.total_kv_tokens, (hipStream_t)stream);
+}
+
+static int dsa_dot(const float* qn, const float* qp, const float* kc, const float* kp,
+                   float* scores, const DsaConfig* cfg, int parts, void* stream) {
+    TRY(dsa_cfg_check(cfg));
+    const DsaConfig& c = *cfg;
+    return launch_dsa_dot(qn, qp, kc, kp, scores, c.num_queries, c.num_heads, c.num_selected_kv,
+                          c.head_dim_compressed, c.head_dim_positional, parts,
+                          (hipStream_t)stream);
+}
+
+int amdmoe_dsa_dot_compressed_f32(const float* q_nope, const float* kc, float* scores,
+                                  const DsaConfig* cfg, void* stream) {
+    return dsa_dot(q_nope, nullptr, kc, nullptr, scores, cfg, 1, stream);
+}
+
+int amdmoe_dsa_dot_positional_f32(const float* q_pe, const float* kp, float* scores,
+                                  const DsaConfig* cfg, void* stream) {
+    return dsa_dot(nullptr, q_pe, nullptr, kp, scores, cfg, 2, stream);
+}
+
+int amdmoe_dsa_dot_fused_f32(const float* q_nope, const float* q_pe, const float* kc,
+                             const float* kp, float* scores, const DsaConfig* cfg, void* stream) {
+    return dsa_dot(q_nope, q_pe, kc, kp, scores, cfg, 3, stream);
+}
+
+int amdmoe_dsa_softmax_f32(float* scores, const DsaConfig* cfg, void* stream) {
+    TRY(dsa_cfg_check(cfg));
+    const DsaConfig& c = *cfg;
+    return launch_dsa_softmax(scores, (long)c.num_queries * c.num_heads, c.num_selected_kv,
+                              (hipStream_t)stream);
+}
+
+int amdmoe_dsa_output_proj_f32(const float* attn, const float* v, float* output,
+                               const DsaConfig* cfg, void* stream) {
+    TRY(dsa_cfg_check(cfg));
+    const DsaConfig& c = *cfg;
+    return launch_dsa_output_proj(attn, v, output, c.num_queries, c.num_heads, c.num_selected_kv,
+                                  c.head_dim_compressed, (hipStream_t)stream);
+}
+
 int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const uint16_t* cache, const int* page_table,
                                  const int* logical_indices, uint16_t* output,

@@ -98,6 +98,24 @@ __device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// ------------------------------------------------------------------ exact order
+// A binary32 product and sum that are never fused into an FMA (hipcc
+// contracts a*b+c by default, and __fmul_rn / __fadd_rn are plain * and +):
+// kernels that reproduce a reference loop's rounding use these.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+// acc + a*b, rounded after the product and after the sum
+__device__ __forceinline__ float mac_rn(float acc, float a, float b) {
+#pragma clang fp contract(off)
+    return acc + a * b;
+}
+
 // ------------------------------------------------------------------ wave ops
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

@@ -53,9 +53,9 @@ __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ q
         const float* kcr = kc + row * Dc;
         const float* kpr = kp + row * Dp;
         float sc = 0.0f, sp = 0.0f;
-        for (int d = 0; d < Dc; d++) sc = __fadd_rn(sc, __fmul_rn(qnr[d], kcr[d]));
-        for (int d = 0; d < Dp; d++) sp = __fadd_rn(sp, __fmul_rn(qpr[d], kpr[d]));
-        s_score[s] = __fmul_rn(__fadd_rn(sc, sp), scale);
+        for (int d = 0; d < Dc; d++) sc = mac_rn(sc, qnr[d], kcr[d]);
+        for (int d = 0; d < Dp; d++) sp = mac_rn(sp, qpr[d], kpr[d]);
+        s_score[s] = mul_rn(add_rn(sc, sp), scale);
     }
     __syncthreads();
     float mx = -FLT_MAX;
@@ -65,13 +65,13 @@ __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ q
     __syncthreads();
     float tot = 0.0f;
     if (lane == 0)
-        for (int s = 0; s < S; s++) tot = __fadd_rn(tot, s_score[s]);
+        for (int s = 0; s < S; s++) tot = add_rn(tot, s_score[s]);
     tot = __shfl(tot, 0, 64);
     for (int s = lane; s < S; s += 64) s_score[s] = __fdiv_rn(s_score[s], tot);
     __syncthreads();
     for (int d = lane; d < Dc; d += 64) {
         float acc = 0.0f;
-        for (int s = 0; s < S; s++) acc = __fadd_rn(acc, __fmul_rn(s_score[s], v[(long)ir[s] * Dc + d]));
+        for (int s = 0; s < S; s++) acc = mac_rn(acc, s_score[s], v[(long)ir[s] * Dc + d]);
         out[(size_t)qh * Dc + d] = acc;
     }
 }

@@ -88,4 +88,14 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
                           int pages_per_seq, hipStream_t st);
 
+// dsa_stages.hip: the reference's DSA stage functions (fp32)
+int launch_dsa_gather(const float* kc, const float* kp, const float* v, const int* idx, float* gkc,
+                      float* gkp, float* gv, int Q, int S, int Dc, int Dp, long N, hipStream_t st);
+// parts: 1 = the K_c dot, 2 = the K_p dot, 3 = both in one accumulator
+int launch_dsa_dot(const float* qn, const float* qp, const float* kc, const float* kp,
+                   float* scores, int Q, int H, int S, int Dc, int Dp, int parts, hipStream_t st);
+int launch_dsa_softmax(float* scores, long rows, int S, hipStream_t st);
+int launch_dsa_output_proj(const float* attn, const float* v, float* out, int Q, int H, int S,
+                           int Dc, hipStream_t st);
+
 }  // namespace amdmoe

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypa
         for (int j = 0; j < n; j++) {
             float v[8];
             Vec8<PT>::load(ypair + ((size_t)t * K + s_ord[j]) * D + 8 * c, v);
-            for (int i = 0; i < 8; i++) acc[i] = __fadd_rn(acc[i], v[i]);
+            for (int i = 0; i < 8; i++) acc[i] = add_rn(acc[i], v[i]);
         }
         if (OUT_BF16) {
             u32x4 o;
@@ -166,7 +166,9 @@ __global__ void scatter_f32_kernel(const float* __restrict__ eo, const int* __re
     float w = 0.0f;
     for (int k = 0; k < K; k++)
         if (idx[(size_t)t * K + k] == expert) { w = wts[(size_t)t * K + k]; break; }
-    out[(size_t)t * D + d] += w * eo[(size_t)m * D + d];
+    // the product is rounded before the sum, as in the reference's atomicAdd
+    float* o = out + (size_t)t * D + d;
+    *o = add_rn(*o, mul_rn(w, eo[(size_t)m * D + d]));
 }
 
 int launch_scatter_f32(const float* expert_out, const int* token_map, const float* wts,

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const float* __restri
     if ((tid & 63) == 0) s_max[tid >> 6] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-    float s = amax > 0.0f ? __fdiv_rn(__fmul_rn(u[bi * cb + bj], amax), 448.0f) : 1.0f;
+    float s = amax > 0.0f ? __fdiv_rn(mul_rn(u[bi * cb + bj], amax), 448.0f) : 1.0f;
     uint8_t* dst = q + (size_t)r * cols + c0;
     for (int j = 0; j < 64; j += 16) {
         u32x4 pk;

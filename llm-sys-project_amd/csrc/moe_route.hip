@@ -66,9 +66,9 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
         if (n == 64) {
 #pragma unroll
             for (int l = 0; l < 64; l++)
-                s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+                s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
         } else {
-            for (int l = 0; l < n; l++) s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+            for (int l = 0; l < n; l++) s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
         }
     }
 #pragma unroll
@@ -116,7 +116,7 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
     // renormalise in slot order (tests/test_moe.cu:65-68)
     float tot = 0.0f;
     for (int k = 0; k < K; k++)
-        tot = __fadd_rn(tot, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), k)));
+        tot = add_rn(tot, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), k)));
     if (lane < K) {
         out_idx[lane] = si;
         out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
@@ -133,7 +133,7 @@ __device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float
     wave_lds_sync();
     float s = 0.0f;
     if (lane == 0)
-        for (int e = 0; e < E; e++) s = __fadd_rn(s, p[e]);
+        for (int e = 0; e < E; e++) s = add_rn(s, p[e]);
     s = __shfl(s, 0, kWave);
     for (int e = lane; e < E; e += kWave) p[e] = __fdiv_rn(p[e], s);
     wave_lds_sync();
@@ -166,7 +166,7 @@ __device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float
         m = argmin_slot(thr);
     }
     float tot = 0.0f;
-    for (int k = 0; k < K; k++) tot = __fadd_rn(tot, __shfl(sv, k, kWave));
+    for (int k = 0; k < K; k++) tot = add_rn(tot, __shfl(sv, k, kWave));
     if (lane < K) {
         out_idx[lane] = si;
         out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
         if (t < T) {
             const XT* xr = x + (size_t)t * D;
             const GT* wr = wg + (size_t)e * D;
-            for (int d = 0; d < D; d++) sum = __fadd_rn(sum, __fmul_rn(load_f(xr + d), load_f(wr + d)));
-            if (bias) sum = __fadd_rn(sum, bias[e]);
+            for (int d = 0; d < D; d++) sum = mac_rn(sum, load_f(xr + d), load_f(wr + d));
+            if (bias) sum = add_rn(sum, bias[e]);
         }
         s_logit[j] = sum;
     }

@@ -58,6 +58,12 @@ def lib():
             "orc_dequant_weight_128x128": (None, [_u8p, _f32p, _I, _I, _f32p]),
             "orc_moe_forward_fp8": (None, [_u16p, _I, _u16p, _u8p, _f32p, _u8p, _f32p,
                                            ctypes.c_void_p, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
+            "orc_dsa_kv_gather": (None, [_f32p, ctypes.c_void_p, _f32p, _i32p, _f32p,
+                                         ctypes.c_void_p, _f32p, _I, _I, _I, _I]),
+            "orc_dsa_dot": (None, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_void_p, _f32p, _I, _I, _I, _I, _I, _I]),
+            "orc_dsa_softmax": (None, [_f32p, _L, _I]),
+            "orc_dsa_output_proj": (None, [_f32p, _f32p, _f32p, _I, _I, _I, _I]),
             "orc_dsa_forward_f32": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _f32p,
                                            _I, _I, _I, _I, _I]),
             "orc_dsa_translate": (None, [_i32p, _i32p, _I, _I, _I, _I, _i32p]),
@@ -271,6 +277,51 @@ def dsa_forward_f32(qn, qp, kc, kp, v, idx):
     S = idx.shape[1]
     out = np.empty((Q, H, Dc), np.float32)
     lib().orc_dsa_forward_f32(qn, qp, kc, kp, v, idx, out, Q, H, Dc, Dp, S)
+    return out
+
+
+def dsa_kv_gather(kc, kp, v, idx):
+    """naive_dsa.cu:13-60 -> (gathered_kc, gathered_kp, gathered_v)."""
+    kc, kp, v = (_c(a, np.float32) for a in (kc, kp, v))
+    idx = _c(idx, np.int32)
+    Q, S = idx.shape
+    Dc, Dp = kc.shape[1], kp.shape[1]
+    gkc = np.empty((Q, S, Dc), np.float32)
+    gkp = np.empty((Q, S, Dp), np.float32)
+    gv = np.empty((Q, S, Dc), np.float32)
+    lib().orc_dsa_kv_gather(kc, kp.ctypes.data if Dp else None, v, idx, gkc,
+                            gkp.ctypes.data if Dp else None, gv, Q, S, Dc, Dp)
+    return gkc, gkp, gv
+
+
+def dsa_dot(qn, qp, kc, kp, scores, parts):
+    """naive_dsa.cu:89-276; parts 1 = compressed, 2 = positional, 3 = fused.
+    Returns scores + the dots (the input is not modified)."""
+    out = _c(scores, np.float32).copy()
+    Q, H, S = out.shape
+    arrs = [None if a is None else _c(a, np.float32) for a in (qn, qp, kc, kp)]
+    Dc = arrs[0].shape[2] if arrs[0] is not None else 0
+    Dp = arrs[1].shape[2] if arrs[1] is not None else 0
+    ptr = [None if a is None else a.ctypes.data for a in arrs]
+    lib().orc_dsa_dot(*ptr, out, Q, H, S, Dc, Dp, parts)
+    return out
+
+
+def dsa_softmax(scores):
+    """naive_dsa.cu:278-296 on a copy of scores [..., S]."""
+    out = _c(scores, np.float32).copy()
+    S = out.shape[-1]
+    lib().orc_dsa_softmax(out, out.size // S if S else 0, S)
+    return out
+
+
+def dsa_output_proj(attn, v):
+    """naive_dsa.cu:300-316: attn [Q,H,S], v [Q,S,Dc] -> [Q,H,Dc]."""
+    attn, v = _c(attn, np.float32), _c(v, np.float32)
+    Q, H, S = attn.shape
+    Dc = v.shape[2]
+    out = np.empty((Q, H, Dc), np.float32)
+    lib().orc_dsa_output_proj(attn, v, out, Q, H, S, Dc)
     return out
 
 

@@ -14,6 +14,11 @@
  *   - random_fill           utils/cuda_utils.cuh:56-60   (glibc rand(), same expression)
  *   - gen_sparse_indices    tests/test_dsa.cu:73-85
  *   - max/mean_abs_error    utils/cuda_utils.cuh:70-85
+ * and the reference's DSA GPU stage kernels (their loops are scalar too):
+ *   - dsa_kv_gather         kernels/dsa/naive_dsa.cu:13-60
+ *   - dsa_dot_*             kernels/dsa/naive_dsa.cu:89-134, 157-206, 208-276
+ *   - dsa_softmax           kernels/dsa/naive_dsa.cu:278-296
+ *   - dsa_output_proj       kernels/dsa/naive_dsa.cu:300-316
  * and adds the BASELINE-defined formats the reference does not have:
  *   - OCP fp8 e4m3 ("E4M3FN") encode/decode, bf16 round-to-nearest-even,
  *   - 1x128 activation / 128x128 weight block quantisation,
@@ -31,7 +36,10 @@
  * (x=0, duplicated gate rows, K=E, E=1); brute-force counting sort for the
  * permutation; float64 textbook GEMM/SwiGLU for the expert FFN; identical
  * experts => y = FFN(x); DSA S=1, q=0, S=N-dense and index-permutation
- * invariance; paged == flat translation.
+ * invariance; paged == flat translation; DSA stages: gather == fancy
+ * indexing, dots and output projection == float64 products (one-hot inputs
+ * exact), softmax == float64 softmax (uniform rows exact), and the stages
+ * composed as naive_dsa.cu:435-474 == cpu_dsa_forward.
  */
 #include <float.h>
 #include <math.h>
@@ -509,6 +517,78 @@ EXPORT void orc_dsa_forward_f32(const float* q_nope, const float* q_pe,
         }
         free(kc); free(kp); free(v); free(scores);
     }
+}
+
+/* The stage functions of naive_dsa.cuh:31-68, in the order of operations of
+ * their kernels (one thread's sequential loop per output value). */
+
+/* naive_dsa.cu:13-60: gathered_*[q,s,:] = cache[idx[q,s], :]. */
+EXPORT void orc_dsa_kv_gather(const float* kv_c, const float* kv_p, const float* v_cache,
+                              const int* idx, float* gkc, float* gkp, float* gv,
+                              int Q, int S, int Dc, int Dp) {
+    for (long r = 0; r < (long)Q * S; r++) {
+        long row = idx[r];
+        memcpy(gkc + r * Dc, kv_c + row * Dc, sizeof(float) * (size_t)Dc);
+        if (Dp > 0) memcpy(gkp + r * Dp, kv_p + row * Dp, sizeof(float) * (size_t)Dp);
+        memcpy(gv + r * Dc, v_cache + row * Dc, sizeof(float) * (size_t)Dc);
+    }
+}
+
+/* naive_dsa.cu:89-134 (parts = 1: q_nope . kc), 157-206 (parts = 2:
+ * q_pe . kp), 208-276 (parts = 3: the concatenation, one accumulator):
+ * sum over d in order, then scores[q,h,s] += sum. */
+EXPORT void orc_dsa_dot(const float* qn, const float* qp, const float* kc, const float* kp,
+                        float* scores, int Q, int H, int S, int Dc, int Dp, int parts) {
+    #pragma omp parallel for schedule(static)
+    for (int q = 0; q < Q; q++)
+        for (int h = 0; h < H; h++)
+            for (int s = 0; s < S; s++) {
+                float sum = 0.0f;
+                if (parts & 1) {
+                    const float* a = qn + ((size_t)q * H + h) * Dc;
+                    const float* b = kc + ((size_t)q * S + s) * Dc;
+                    for (int d = 0; d < Dc; d++) sum += a[d] * b[d];
+                }
+                if (parts & 2) {
+                    const float* a = qp + ((size_t)q * H + h) * Dp;
+                    const float* b = kp + ((size_t)q * S + s) * Dp;
+                    for (int d = 0; d < Dp; d++) sum += a[d] * b[d];
+                }
+                scores[((size_t)q * H + h) * S + s] += sum;
+            }
+}
+
+/* naive_dsa.cu:278-296: per row, e = expf(x - max) (summed in order), then
+ * x = e * (1 / sum).  (The CPU oracle of tests/test_dsa.cu divides instead.) */
+EXPORT void orc_dsa_softmax(float* scores, long rows, int S) {
+    #pragma omp parallel for schedule(static)
+    for (long r = 0; r < rows; r++) {
+        float* row = scores + r * S;
+        float mx = -FLT_MAX;
+        for (int s = 0; s < S; s++) mx = fmaxf(mx, row[s]);
+        float sum = 0.0f;
+        for (int s = 0; s < S; s++) {
+            row[s] = expf(row[s] - mx);
+            sum += row[s];
+        }
+        float inv = 1.0f / sum;
+        for (int s = 0; s < S; s++) row[s] *= inv;
+    }
+}
+
+/* naive_dsa.cu:300-316: out[q,h,d] = sum over s in order of
+ * attn[q,h,s] * v[q,s,d]. */
+EXPORT void orc_dsa_output_proj(const float* attn, const float* v, float* out,
+                                int Q, int H, int S, int Dc) {
+    #pragma omp parallel for schedule(static)
+    for (int q = 0; q < Q; q++)
+        for (int h = 0; h < H; h++)
+            for (int d = 0; d < Dc; d++) {
+                float sum = 0.0f;
+                for (int s = 0; s < S; s++)
+                    sum += attn[((size_t)q * H + h) * S + s] * v[((size_t)q * S + s) * Dc + d];
+                out[((size_t)q * H + h) * Dc + d] = sum;
+            }
 }
 
 /* Paged address translation (BASELINE DSA config; the reference has no page

@@ -383,3 +383,93 @@ def test_reference_dsa_cases_match_float64(orc, name, shape, tol):
     qn, qp, kc, kp, v, idx = orc.reference_dsa_inputs(Q, H, Dc, Dp, S, P, N)
     out = orc.dsa_forward_f32(qn, qp, kc, kp, v, idx)
     np.testing.assert_allclose(out, _dsa64(qn, qp, kc, kp, v, idx), rtol=1e-4, atol=1e-6)
+
+
+# ---------------------------------------------------------------- DSA stages
+def _stage_inputs(orc, seed=3, Q=3, H=5, Dc=40, Dp=12, S=17, N=64):
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    idx = rng.integers(0, N, (Q, S)).astype(np.int32)
+    return f(Q, H, Dc), f(Q, H, Dp), f(N, Dc), f(N, Dp), f(N, Dc), idx
+
+
+def test_dsa_gather_is_fancy_indexing(orc):
+    qn, qp, kc, kp, v, idx = _stage_inputs(orc)
+    gkc, gkp, gv = orc.dsa_kv_gather(kc, kp, v, idx)
+    np.testing.assert_array_equal(gkc, kc[idx])
+    np.testing.assert_array_equal(gkp, kp[idx])
+    np.testing.assert_array_equal(gv, v[idx])
+    # Dp = 0: no positional part
+    g0 = orc.dsa_kv_gather(kc, np.zeros((64, 0), np.float32), v, idx)
+    assert g0[1].shape == (3, 17, 0)
+
+
+def test_dsa_dots_match_float64_and_accumulate(orc):
+    qn, qp, kc, kp, v, idx = _stage_inputs(orc)
+    gkc, gkp, _ = orc.dsa_kv_gather(kc, kp, v, idx)
+    init = np.random.default_rng(4).standard_normal((3, 5, 17)).astype(np.float32)
+    dc = np.einsum("qhd,qsd->qhs", qn.astype(np.float64), gkc)
+    dp = np.einsum("qhd,qsd->qhs", qp.astype(np.float64), gkp)
+    for parts, ref in ((1, dc), (2, dp), (3, dc + dp)):
+        out = orc.dsa_dot(qn if parts & 1 else None, qp if parts & 2 else None,
+                          gkc if parts & 1 else None, gkp if parts & 2 else None, init, parts)
+        np.testing.assert_allclose(out, init + ref, rtol=1e-5, atol=1e-5)
+    # one-hot queries pick one column of the gathered rows, exactly
+    oh = np.zeros_like(qn)
+    oh[:, :, 7] = 1.0
+    out = orc.dsa_dot(oh, None, gkc, None, np.zeros((3, 5, 17), np.float32), 1)
+    np.testing.assert_array_equal(out, np.repeat(gkc[:, None, :, 7], 5, 1))
+    ohp = np.zeros_like(qp)
+    ohp[:, :, 3] = 1.0
+    out = orc.dsa_dot(np.zeros_like(qn), ohp, gkc, gkp, np.zeros((3, 5, 17), np.float32), 3)
+    np.testing.assert_array_equal(out, np.repeat(gkp[:, None, :, 3], 5, 1))
+
+
+def test_dsa_dot_sums_in_d_order(orc):
+    # (1 + 1e8) - 1e8 = 0 in binary32 summed front to back; any other order
+    # of these three terms gives 1
+    qn = np.ones((1, 1, 3), np.float32)
+    kc = np.array([[[1.0, 1e8, -1e8]]], np.float32)
+    out = orc.dsa_dot(qn, None, kc, None, np.zeros((1, 1, 1), np.float32), 1)
+    assert out[0, 0, 0] == 0.0
+    # fused: the positional terms continue the same accumulator
+    qp = np.ones((1, 1, 1), np.float32)
+    out = orc.dsa_dot(np.ones((1, 1, 2), np.float32), qp, np.array([[[1.0, 1e8]]], np.float32),
+                      np.array([[[-1e8]]], np.float32), np.zeros((1, 1, 1), np.float32), 3)
+    assert out[0, 0, 0] == 0.0
+
+
+def test_dsa_softmax_matches_float64(orc):
+    rng = np.random.default_rng(6)
+    x = (3 * rng.standard_normal((4, 3, 50))).astype(np.float32)
+    p = orc.dsa_softmax(x)
+    x64 = x.astype(np.float64)
+    ref = np.exp(x64 - x64.max(-1, keepdims=True))
+    ref /= ref.sum(-1, keepdims=True)
+    np.testing.assert_allclose(p, ref, rtol=1e-6, atol=1e-8)
+    # uniform rows, S a power of two: exactly 1/S
+    np.testing.assert_array_equal(orc.dsa_softmax(np.full((2, 2, 64), 0.25, np.float32)),
+                                  np.full((2, 2, 64), 1 / 64, np.float32))
+
+
+def test_dsa_output_proj_matches_float64(orc):
+    rng = np.random.default_rng(7)
+    attn = rng.random((2, 3, 20)).astype(np.float32)
+    v = rng.standard_normal((2, 20, 9)).astype(np.float32)
+    out = orc.dsa_output_proj(attn, v)
+    np.testing.assert_allclose(out, np.einsum("qhs,qsd->qhd", attn.astype(np.float64), v),
+                               rtol=1e-5, atol=1e-6)
+    one = np.zeros_like(attn)
+    one[:, :, 11] = 1.0
+    np.testing.assert_array_equal(orc.dsa_output_proj(one, v), np.repeat(v[:, None, 11], 3, 1))
+
+
+def test_dsa_stages_compose_to_forward(orc):
+    # naive_dsa.cu:435-474: gather, fused dot into zeroed scores, scale,
+    # softmax, output projection == cpu_dsa_forward (tests/test_dsa.cu:23-68)
+    qn, qp, kc, kp, v, idx = orc.reference_dsa_inputs(4, 4, 64, 16, 64, 16, 256)
+    gkc, gkp, gv = orc.dsa_kv_gather(kc, kp, v, idx)
+    s = orc.dsa_dot(qn, qp, gkc, gkp, np.zeros((4, 4, 64), np.float32), 3)
+    s = s * np.float32(1.0 / math.sqrt(64 + 16))
+    out = orc.dsa_output_proj(orc.dsa_softmax(s), gv)
+    np.testing.assert_allclose(out, orc.dsa_forward_f32(qn, qp, kc, kp, v, idx), rtol=1e-5, atol=1e-6)
