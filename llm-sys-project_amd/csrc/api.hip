@@ -509,11 +509,17 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const DsaConfig* cfg, int pages_per_seq, void* stream) {
     AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
     const DsaConfig& c = *cfg;
+    AMDMOE_CHECK_ARG(c.num_queries >= 0 && c.num_heads >= 1 && c.num_selected_kv >= 1,
+                     "bad DsaConfig");
+    // the token-split partials live in a private buffer of the cached workspace
+    const size_t need = dsa_paged_scratch_bytes(c.num_queries, c.num_heads, c.num_selected_kv);
+    void* scratch = nullptr;
+    if (need) TRY(cached_workspace(need, &scratch));
     return launch_dsa_bf16_paged(q_nope, q_pe, cache, c.total_kv_tokens, page_table,
                                  logical_indices, output, c.num_queries, c.num_heads,
                                  c.head_dim_compressed,
                                  c.head_dim_positional, c.num_selected_kv, c.page_size,
-                                 pages_per_seq, (hipStream_t)stream);
+                                 pages_per_seq, scratch, need, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -62,8 +62,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Two floats -> two bf16 (a in the low half), round to nearest even: the
+// gfx950 v_cvt_pk_bf16_f32 (same results as f32_to_bf16 for every non-NaN
+// input; NaNs stay NaNs).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 // Four floats -> four OCP e4m3 bytes (RNE).  Inputs are pre-clamped to

@@ -105,6 +105,11 @@ int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const floa
 //   O^T (512 d x 16 heads) += V^T . P^T : 32 MFMA 16x16x16; P^T comes
 //   straight from S^T's output layout (lane = head, 4 tokens), V^T
 //   fragments from the row-major K_c tile with ds_read_b64_tr_b16.
+// Out-of-range voffset for the cache loads: at least the buffer size (the
+// cache is at most kMaxCacheBytes) and far enough below 2^32 that adding the
+// largest soffset and the 16-byte access cannot wrap back into range.
+constexpr uint32_t kOobDsa = 0xFFFFF000u;
+constexpr long kMaxCacheBytes = 0xFFFFE000L;
 constexpr int kDc = 512, kDp = 64, kDt = 576;
 constexpr int kRowBytes = kDt * 2;               // 1152
 constexpr int kRowChunks = kRowBytes / 16;       // 72
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
             const int c = 64 * (kLoadsPerWave * wave + n) + lane;
             const int r = c / kRowChunks, jp = c - r * kRowChunks;
             const int j = jp ^ (r & 7);
-            const uint32_t vo = row[n] >= 0 ? (uint32_t)((long)row[n] * kRowBytes + 16 * j) : kOob;
+            const uint32_t vo = row[n] >= 0 ? (uint32_t)((long)row[n] * kRowBytes + 16 * j) : kOobDsa;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc, (lds_ptr_t)(base + 1024 * (kLoadsPerWave * wave + n)), 16, vo, 0, 0, 0);
         }
@@ -415,7 +420,7 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
     // shift the LDS destination.
     auto tile_vo = [&](int tile) {
         const int tok = tile * kT64 + my_tok;
-        return tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * my_chunk) : kOob;
+        return tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * my_chunk) : kOobDsa;
     };
     auto issue_n = [&](int st, uint32_t vo, int n) __attribute__((always_inline)) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -584,28 +589,426 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
     }
 }
 
+// ------------------------------------------------------ split kernel
+// dsa_split_kernel (H a multiple of 128): one workgroup per (query, group
+// of 128 heads, token split), 4 waves; wave w owns heads 32w..32w+31 of the
+// group for all of the split's tokens, so its softmax state is private (no
+// exchange between waves) and P goes from the S^T accumulators straight
+// into the PV MFMA operand.  32-token tiles stream through a 4-stage LDS
+// ring (three tiles in flight), filled by direct global->LDS loads; each
+// wave reads every tile once for S and once for V.
+//   S^T (16 tokens x 16 heads) = K . Q^T   16x16x32 bf16, 2 token x 2 head
+//                                          tiles, q of 32 heads in registers
+//   online softmax per head in the exp2 domain; l is kept per lane and
+//     reduced once at the end
+//   O^T (512 dims x 16 heads) += V^T . P^T  16x16x32 bf16 in the token
+//     order of S^T's output layout: lane (head c, group g) holds tokens
+//     4g..4g+3 and 16+4g..16+4g+3, and the transposed LDS reads of V^T
+//     fetch the same tokens
+// Registers: O is 256 accumulators (the whole AGPR file) and q 144 VGPRs,
+// so (1) the S^T MFMAs write VGPRs, and (2) O is never read or written by
+// the VALU (which would make the compiler shuttle all of it between register
+// files): O leaves the AGPRs only through stores.  The running max m is
+// raised only when a tile max exceeds it by more than 8 (so p <= 256); then
+// the wave stores O to its spare rows B, adds B into its partial rows A in
+// memory, scaled to the new max, and restarts O at zero.  This is a rare
+// path: with O(1) scores the first tile's max is never exceeded by 8.
+// Every split writes its unnormalised O (fp32, rows A) and (max, sum) per
+// head; dsa_merge_kernel combines the splits and writes bf16.
+//
+// Tile layout (tile32_off): 1 KB blocks of 16 tokens x 4 chunks (16-byte
+// chunk j of the 1152-byte row), blocks [token group][chunk group], within a
+// block [token][slot] with slot = (j & 3) ^ hsw(token bits 2-3).  hsw swaps
+// the two bits, which keeps the 16-token fragment reads of S conflict-free
+// and puts the two 4-token groups of a transposed V read in different halves
+// of each 64-byte window.
+constexpr int kT32 = 32;
+constexpr int kStage32 = kT32 * kRowBytes;                // 36864
+constexpr int kRing32 = 4;
+constexpr int kMaxChunk = 2048;                           // tokens per split
+constexpr int kRows32Off = kRing32 * kStage32;            // 147456
+constexpr int kDsaSplitLds = kRows32Off + kMaxChunk * 4;  // 155648
+
+__device__ __forceinline__ int hsw(int a) { return ((a & 1) << 1) | (a >> 1); }
+__device__ __forceinline__ int tile32_off(int t, int j) {  // token t (0..31), chunk j (0..71)
+    return ((t >> 4) * 18 + (j >> 2)) * 1024 + (t & 15) * 64 + (((j & 3) ^ hsw((t >> 2) & 3)) << 4);
+}
+
+// Four VGPR-form MFMAs of one S^T K-step (token tiles x head tiles), as asm
+// with the wait states the compiler would add for them: 2 after a VALU
+// write of an operand (leading s_nop 1); FIRST: accumulators start at 0;
+// LAST: 16 wait states before any other instruction reads the results.
+template <bool FIRST, bool LAST>
+__device__ __forceinline__ void s_mfma4(f32x4 (&c)[2][2], const u32x4& a0, const u32x4& a1,
+                                        const u32x4& q0, const u32x4& q1) {
+    if (FIRST)
+        asm volatile(
+            "s_nop 1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, 0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, 0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, 0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, 0"
+            : "=&v"(c[0][0]), "=&v"(c[0][1]), "=&v"(c[1][0]), "=&v"(c[1][1])
+            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
+    else if (!LAST)
+        asm volatile(
+            "s_nop 1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, %0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, %1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, %2\n\t"
+            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, %3"
+            : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])
+            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
+    else
+        asm volatile(
+            "s_nop 1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, %0\n\t"
+            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, %1\n\t"
+            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, %2\n\t"
+            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, %3\n\t"
+            "s_nop 7\n\t"
+            "s_nop 7"
+            : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])
+            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
+}
+
+__global__ __launch_bounds__(256, 1) void dsa_split_kernel(
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
+    const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
+    const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,
+    float* __restrict__ part_ml, int H,
+    int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    int* s_rows = (int*)(smem + kRows32Off);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hgroups = H / 128;
+    const int sp = blockIdx.x % nsplit;
+    const int qh = blockIdx.x / nsplit;
+    const int hg = qh % hgroups, qi = qh / hgroups;
+    const int t0 = sp * chunk;
+    const int len = max(0, min(S, t0 + chunk) - t0);
+    const int g = lane >> 4, c16 = lane & 15;
+    const int hbase = 128 * hg + 32 * wave;  // this wave's first head
+
+    u32x4 qf[2][18];
+#pragma unroll
+    for (int ht = 0; ht < 2; ht++) {
+        const size_t hrow = (size_t)qi * H + hbase + 16 * ht + c16;
+        const uint16_t* qnr = qn + hrow * kDc;
+        const uint16_t* qpr = qp + hrow * kDp;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qf[ht][ks] = *(const u32x4*)(qnr + 32 * ks + 8 * g);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) qf[ht][16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
+    }
+    // page-table translation of the split's logical indices (an index
+    // outside the sequence gives row -1: a zero row)
+    {
+        const int* lg = logical + (size_t)qi * S + t0;
+        const int* pt = page_table + (size_t)qi * pages_per_seq;
+        const long seq = (long)pages_per_seq * page;
+        for (int i = tid; i < len; i += 256) {
+            const int li = lg[i];
+            s_rows[i] = (li >= 0 && li < seq) ? pt[li / page] * page + li % page : -1;
+        }
+    }
+    // q of heads hbase + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
+    __syncthreads();  // s_rows visible; regular loads complete
+
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
+    // DMA: block b of a tile is filled by one instruction, lane l taking
+    // token 16 (b / 18) + (l >> 2), chunk 4 (b % 18) + ((l & 3) ^ hsw(l >> 4));
+    // wave w issues blocks w, w + 4, ..., w + 32.  The chunk-group offset goes
+    // in soffset (an instruction immediate would also move the LDS address).
+    const uint32_t lane_c16 = 16u * (uint32_t)((lane & 3) ^ hsw((lane >> 4) & 3));
+    auto row_vo = [&](int tok) __attribute__((always_inline)) {
+        uint32_t vo = kOobDsa;
+        if (tok < len) {
+            const long r = s_rows[tok];
+            const long off = r * kRowBytes + lane_c16;
+            if (r >= 0 && off < cache_bytes) vo = (uint32_t)off;
+        }
+        return vo;
+    };
+    auto issue_blk = [&](int st, uint32_t vo0, uint32_t vo1, int n) __attribute__((always_inline)) {
+        const int b = wave + 4 * n;
+        const int tg = b >= 18 ? 1 : 0;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rc, (lds_ptr_t)(smem + st * kStage32 + b * 1024), 16, tg ? vo1 : vo0, 64 * (b - 18 * tg), 0, 0);
+    };
+
+    f32x4 o[32][2];  // dims 16mt + 4g + i, head hbase + 16ht + c16
+#pragma unroll
+    for (int i = 0; i < 32; i++)
+        for (int j = 0; j < 2; j++) o[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // This wave's partial rows A (and spare rows B): per (query, split) H
+    // heads x 512 dims, each 16-head block stored in the accumulator order
+    // [dim tile mt][lane][4] (element (dim 16mt + 4g + i, head c16)), so a
+    // tile is one contiguous 1 KB store.
+    const size_t prow0 = ((size_t)qi * nsplit + sp) * H + hbase;
+    const size_t lane_off = (size_t)lane * 4;  // + 16 kDc ht + 256 mt
+    // O -> rows (A or B), straight from the accumulators; the base is made
+    // opaque so the addresses are formed here, not hoisted and kept live
+    auto store_o = [&](float* rows) __attribute__((always_inline)) {
+        float* base = rows + prow0 * kDc + lane_off;
+        asm volatile("" : "+v"(base));
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++)
+#pragma unroll
+            for (int mt = 0; mt < 32; mt++) *(f32x4*)(base + 16 * kDc * ht + 256 * mt) = o[mt][ht];
+    };
+    // A = (first ? 0 : A) + B, times c[ht], in memory
+    auto fold_b = [&](bool first, const float (&c)[2]) __attribute__((always_inline)) {
+        float* a = part_o + prow0 * kDc + lane_off;
+        const float* b = spare_o + prow0 * kDc + lane_off;
+        asm volatile("" : "+v"(a), "+v"(b));
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++)
+#pragma unroll 4
+            for (int mt = 0; mt < 32; mt++) {
+                const size_t off = 16 * kDc * ht + 256 * mt;
+                f32x4 v = *(const f32x4*)(b + off);
+                if (!first) v += *(const f32x4*)(a + off);
+                *(f32x4*)(a + off) = v * c[ht];
+            }
+    };
+    float m_run[2] = {-INFINITY, -INFINITY}, l_lane[2] = {0.f, 0.f};
+    bool flushed = false;  // uniform: part of O is in the partial rows
+    const int ntiles = (len + kT32 - 1) / kT32;
+
+    const int koff = tile32_off(c16, g);  // S fragment (token tile tt, K-step ks): + 1024 (18 tt + ks)
+    int vlo[2];                           // V^T read, dim tile mt: vlo[mt & 1] + 1024 (mt >> 1)
+#pragma unroll
+    for (int e = 0; e < 2; e++)
+        vlo[e] = tile32_off(4 * g + (c16 >> 2), 2 * e + ((c16 >> 1) & 1)) + 8 * (c16 & 1);
+
+    // prologue: tiles 0..2 (tiles past the end read zeros into their stage,
+    // so every iteration waits for the same count)
+#pragma unroll
+    for (int i = 0; i < kRing32 - 1; i++) {
+        const uint32_t a = row_vo(kT32 * i + (lane >> 2)), b = row_vo(kT32 * i + 16 + (lane >> 2));
+#pragma unroll
+        for (int n = 0; n < 9; n++) issue_blk(i, a, b, n);
+    }
+    for (int t = 0; t < ntiles; t++) {
+        const int tn = t + kRing32 - 1;
+        const uint32_t nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
+        wait_vmcnt<9 * (kRing32 - 2)>();  // tile t landed (this wave's part)
+        bare_barrier();                   // ... everywhere; stage tn % 4 is free
+        uint32_t soff = (t % kRing32) * kStage32;
+        asm volatile("" : "+s"(soff));
+        const uint8_t* kb = smem + soff;
+        const int stn = tn % kRing32;
+
+        // S^T, 18 K-steps; fragment reads kPre steps ahead; one load of tile
+        // tn goes out per step for the first 9
+        f32x4 sacc[2][2];
+        {
+            constexpr int kPre = 6;
+            u32x4 a[18][2];
+#pragma unroll
+            for (int ks = 0; ks < kPre; ks++)
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) a[ks][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks));
+            static_for<18>([&](auto ksc) __attribute__((always_inline)) {
+                constexpr int ks = decltype(ksc)::value;
+                if constexpr (ks + kPre < 18)
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++)
+                        a[ks + kPre][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks + kPre));
+                s_mfma4<ks == 0, ks == 17>(sacc, a[ks][0], a[ks][1], qf[0][ks], qf[1][ks]);
+                if (ks < 9) issue_blk(stn, nvo0, nvo1, ks);
+                // keep the prefetch depth as written: with O and q resident,
+                // hoisted fragment reads would spill
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        // lane: head 16ht + c16, tokens 16tt + 4g + i of the tile
+        float sv[2][2][4], tm[2];
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++) {
+            tm[ht] = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tk = kT32 * t + 16 * tt + 4 * g + i;
+                    sv[tt][ht][i] = tk < len ? sacc[tt][ht][i] * scale_log2 : -INFINITY;
+                    tm[ht] = fmaxf(tm[ht], sv[tt][ht][i]);
+                }
+            tm[ht] = xor32_max(xor16_max(tm[ht]));
+        }
+        const bool first = m_run[0] == -INFINITY;  // uniform: tile 0 (it has a live token)
+        const bool raise = tm[0] > m_run[0] + 8.0f || tm[1] > m_run[1] + 8.0f;
+        if (first) {
+            m_run[0] = tm[0];
+            m_run[1] = tm[1];
+        } else if (__ballot(raise)) {
+            // rare: A = (A + O) scaled to the new max, O restarts at zero
+            float corr[2];
+#pragma unroll
+            for (int ht = 0; ht < 2; ht++) {
+                const float m_new = fmaxf(m_run[ht], tm[ht]);
+                corr[ht] = exp2f(m_run[ht] - m_new);
+                l_lane[ht] *= corr[ht];
+                m_run[ht] = m_new;
+            }
+            store_o(spare_o);
+            fold_b(!flushed, corr);
+#pragma unroll
+            for (int ht = 0; ht < 2; ht++)
+#pragma unroll
+                for (int mt = 0; mt < 32; mt++) o[mt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            flushed = true;
+        }
+        u32x4 pb[2];
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++) {
+            float p[2][4];
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    // the hardware exp2 (0 for a masked -inf score)
+                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][ht][i] - m_run[ht]);
+                    l_lane[ht] += p[tt][i];
+                }
+            pb[ht] = (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                             pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+        }
+        auto vfrag = [&](int mt) __attribute__((always_inline)) {
+            const uint8_t* p = kb + vlo[mt & 1] + 1024 * (mt >> 1);
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)p);
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p + 18 * 1024));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+            return (u32x4){l2[0], l2[1], h2[0], h2[1]};
+        };
+        constexpr int kPreV = 10;
+        u32x4 va[32];
+#pragma unroll
+        for (int mt = 0; mt < kPreV; mt++) va[mt] = vfrag(mt);
+#pragma unroll
+        for (int mt = 0; mt < 32; mt++) {
+            if (mt + kPreV < 32) va[mt + kPreV] = vfrag(mt + kPreV);
+            o[mt][0] = mfma_bf16(va[mt], pb[0], o[mt][0]);
+            o[mt][1] = mfma_bf16(va[mt], pb[1], o[mt][1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wait_vmcnt<0>();  // the trailing (out-of-range) tile loads
+
+    // the split's partial: A = O (+ A if part of O was flushed), m, l
+    if (!flushed) {
+        store_o(part_o);
+    } else {
+        store_o(spare_o);
+        const float one[2] = {1.0f, 1.0f};
+        fold_b(false, one);
+    }
+#pragma unroll
+    for (int ht = 0; ht < 2; ht++) {
+        const float l = xor32_sum(xor16_sum(l_lane[ht]));
+        if (g == 0) *(float2*)(part_ml + 2 * (prow0 + 16 * ht + c16)) = make_float2(m_run[ht], l);
+    }
+}
+
+// Combines the splits of dsa_split_kernel: per (query, head), m = max of
+// the split maxima, weights c_j = 2^(m_j - m), out = (sum c_j O_j) /
+// (sum c_j l_j), bf16.  Workgroup = one query x 16 heads (one partial block),
+// wave w = dim tiles 8w..8w+7 in the block's accumulator order: every load
+// is 1 KB contiguous, and lane (g, c) holds dims 16mt + 4g + i of head c.
+__global__ __launch_bounds__(256) void dsa_merge_kernel(const float* __restrict__ part_o,
+                                                        const float* __restrict__ part_ml,
+                                                        uint16_t* __restrict__ out, int H,
+                                                        int nsplit) {
+    const int h16 = H / 16;
+    const int qi = blockIdx.x / h16, hb = blockIdx.x % h16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int h = 16 * hb + c16;
+    float m = -INFINITY;
+    for (int j = 0; j < nsplit; j++) m = fmaxf(m, part_ml[2 * (((size_t)qi * nsplit + j) * H + h)]);
+    f32x4 acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float L = 0.0f;
+    for (int j = 0; j < nsplit; j++) {
+        const size_t blk = ((size_t)qi * nsplit + j) * H + 16 * hb;  // first row of the block
+        const float2 ml = *(const float2*)(part_ml + 2 * (blk + c16));
+        const float c = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - m);
+        L += c * ml.y;
+        const f32x4* po = (const f32x4*)(part_o + blk * kDc) + 64 * 8 * wave + lane;
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc[k] += c * po[64 * k];
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    uint16_t* orow = out + ((size_t)qi * H + h) * kDc + 4 * g;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int mt = 8 * wave + k;
+        const u32x2 pk = {pack_bf16x2(acc[k][0] * inv, acc[k][1] * inv),
+                          pack_bf16x2(acc[k][2] * inv, acc[k][3] * inv)};
+        *(u32x2*)(orow + 16 * mt) = pk;
+    }
+}
+
+// Splits per query for dsa_split_kernel: enough workgroups to cover the
+// chip (256 CUs), at most 2048 tokens per split, at least 32.
+static int dsa_nsplit(int Q, int H, int S) {
+    const long wg = (long)Q * (H / 128);
+    int ns = (int)std::min<long>((256 + wg - 1) / wg, (S + kT32 - 1) / kT32);
+    return std::max(ns, (S + kMaxChunk - 1) / kMaxChunk);
+}
+
+size_t dsa_paged_scratch_bytes(int Q, int H, int S) {
+    if (Q <= 0 || H % 128 != 0 || S < 1) return 0;  // the kernels without splits
+    const size_t rows = (size_t)Q * dsa_nsplit(Q, H, S) * H;
+    return 2 * rows * kDc * 4 + align_up(rows * 8, 256);  // rows A, spare rows B, (m, l)
+}
+
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
                           long cache_tokens, const int* page_table, const int* logical,
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
-                          int pages_per_seq, hipStream_t st) {
+                          int pages_per_seq, void* scratch, size_t scratch_bytes, hipStream_t st) {
     AMDMOE_CHECK_ARG(Dc == kDc && Dp == kDp, "dsa_decode_bf16_paged: needs Dc=512, Dp=64 (got %d, %d)", Dc, Dp);
     AMDMOE_CHECK_ARG(H % 32 == 0 && H > 0, "dsa_decode_bf16_paged: H=%d not a multiple of 32", H);
     AMDMOE_CHECK_ARG(S >= 1 && S <= kMaxS, "dsa_decode_bf16_paged: S=%d outside [1, %d]", S, kMaxS);
     AMDMOE_CHECK_ARG(page >= 1 && pages_per_seq >= 1, "dsa_decode_bf16_paged: bad paging");
-    AMDMOE_CHECK_ARG(cache_tokens >= 1 && cache_tokens * kRowBytes <= 0xFFFFFFF0L,
+    AMDMOE_CHECK_ARG(cache_tokens >= 1 && cache_tokens * kRowBytes <= kMaxCacheBytes,
                      "dsa_decode_bf16_paged: cache of %ld tokens outside (0, 4 GiB)", cache_tokens);
     if (Q == 0) return AMDMOE_OK;
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_bf16_paged_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kDsaLds));
-        attr_set = true;
-    }
-    // blocks = Q * H/32, padded to a multiple of 8 for the XCD remap; the
-    // padding blocks map past the last query and exit
-    const int nblk = Q * (H / 32);
-    const int grid = (nblk + 7) / 8 * 8;
     const float scale_log2 = 1.0f / sqrtf((float)(Dc + Dp)) * 1.4426950408889634f;
+    if (H % 128 == 0) {
+        const int ns = dsa_nsplit(Q, H, S);
+        const int chunk = (int)ceil_div(ceil_div(S, ns), kT32) * kT32;
+        const size_t need = dsa_paged_scratch_bytes(Q, H, S);
+        AMDMOE_CHECK_ARG(scratch != nullptr && scratch_bytes >= need,
+                         "dsa_decode_bf16_paged: scratch of %zu bytes, %zu needed", scratch_bytes, need);
+        const long grid = (long)Q * (H / 128) * ns;
+        AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_decode_bf16_paged: grid too large");
+        static bool attr_split = false;
+        if (!attr_split) {
+            AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_split_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDsaSplitLds));
+            attr_split = true;
+        }
+        const size_t rows_bytes = (size_t)Q * ns * H * kDc * 4;
+        float* part_o = (float*)scratch;
+        float* spare_o = (float*)((uint8_t*)scratch + rows_bytes);
+        float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes);
+        hipLaunchKernelGGL(dsa_split_kernel, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
+                           qp, cache, cache_tokens * kRowBytes, page_table, logical, part_o, spare_o,
+                           part_ml, H, S, page, pages_per_seq, ns, chunk, scale_log2);
+        AMDMOE_LAUNCH_CHECK();
+        hipLaunchKernelGGL(dsa_merge_kernel, dim3((unsigned)((long)Q * (H / 16))), dim3(256), 0, st,
+                           (const float*)part_o, (const float*)part_ml, out, H, ns);
+        AMDMOE_LAUNCH_CHECK();
+        return AMDMOE_OK;
+    }
+    // H not a multiple of 128: one workgroup per (query, 32 heads)
+    const int nblk = Q * (H / 32);
+    const int grid = (nblk + 7) / 8 * 8;  // padded for the XCD remap; padding blocks exit
     if (S <= kMaxS64) {
         static bool attr64_set = false;
         if (!attr64_set) {
@@ -618,6 +1021,12 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                            pages_per_seq, scale_log2);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
+    }
+    static bool attr_set = false;
+    if (!attr_set) {
+        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_bf16_paged_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kDsaLds));
+        attr_set = true;
     }
     hipLaunchKernelGGL(dsa_bf16_paged_kernel, dim3(grid), dim3(256), kDsaLds, st, qn, qp, cache,
                        cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,

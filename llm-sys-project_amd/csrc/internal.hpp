@@ -83,10 +83,13 @@ int launch_scatter_f32(const float* expert_out, const int* token_map, const floa
 int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const float* kp,
                    const float* v, const int* idx, float* out, int Q, int H, int Dc, int Dp, int S,
                    int N, hipStream_t st);
+// scratch: dsa_paged_scratch_bytes(Q, H, S) bytes (split partials), may be
+// 0 bytes / nullptr when that is 0
+size_t dsa_paged_scratch_bytes(int Q, int H, int S);
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
                           long cache_tokens, const int* page_table, const int* logical,
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,
-                          int pages_per_seq, hipStream_t st);
+                          int pages_per_seq, void* scratch, size_t scratch_bytes, hipStream_t st);
 
 // dsa_stages.hip: the reference's DSA stage functions (fp32)
 int launch_dsa_gather(const float* kc, const float* kp, const float* v, const int* idx, float* gkc,

@@ -38,9 +38,11 @@ def test_dsa_f32_reference_cases(amd, orc, name, shape, tol):
     assert err < 1e-6
 
 
-def _paged_case(amd, orc, Q, H, S, ctx, page=64, check_q=None, seed=5):
+def _paged_case(amd, orc, Q, H, S, ctx, page=64, check_q=None, seed=5, inputs=None):
     import synth
-    qn, qp, cache, pt, logical, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=seed)
+    if inputs is None:
+        inputs = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=seed)
+    qn, qp, cache, pt, logical, pps = inputs
     out = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
     amd.dsa_decode_bf16_paged(qn, qp, cache, pt, logical, out,
                               amd.dsa_config(Q, H, 512, 64, S, page, Q * ctx), pps)
@@ -78,3 +80,48 @@ def test_dsa_bf16_paged_baseline_shape(amd, orc):
     """B=64, H=128, S=2048 of 32768-token contexts; 4 queries checked."""
     print("dsa_bf16 baseline", flush=True)
     assert _paged_case(amd, orc, 64, 128, 2048, 32768, check_q=[0, 17, 42, 63]) < 1e-2
+
+
+# H a multiple of 128: the token-split kernel (workgroup = query x 128 heads
+# x split) plus the merge of the splits
+@pytest.mark.parametrize("Q,H,S,ctx", [
+    (8, 128, 100, 512),    # 4 splits of 32, the last one 4 tokens
+    (3, 128, 1, 128),      # one token
+    (2, 256, 3000, 4096),  # 2 head groups; 64 splits of 64 tokens, the last 17 empty
+    (300, 128, 64, 128),   # one split per query (no token split)
+    (64, 128, 512, 1024),  # 4 splits of 4 tiles
+])
+def test_dsa_bf16_paged_split_shapes(amd, orc, Q, H, S, ctx):
+    print(f"dsa_bf16 split Q={Q} H={H} S={S}", flush=True)
+    check = None if Q <= 8 else [0, Q // 2, Q - 1]
+    assert _paged_case(amd, orc, Q, H, S, ctx, check_q=check, seed=Q + S) < 1e-2
+
+
+def test_dsa_bf16_paged_split_max_jumps(amd, orc):
+    """Scores that jump by more than 8 (log2 units) between tiles of a split:
+    the path that moves O out of the accumulators and rescales it in memory.
+    Scores come from q_pe . K_p only (q_nope = 0), values from K_c: in every
+    128-token split, tile 1 and tile 3 open with a token whose score is
+    9.6 resp. 19.2 above the rest and whose V row is -1 (all other V rows
+    +1), so the output depends on every tile's share."""
+    import synth
+    print("dsa_bf16 split max jumps", flush=True)
+    Q, H, S, ctx, page = 64, 128, 512, 1024, 64
+    qn, qp, cache, pt, logical, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=9)
+    bf = lambda v: torch.tensor(v, dtype=torch.float32).to(torch.bfloat16).view(torch.int16)
+    qn = torch.zeros_like(qn)
+    qp = bf(1.0).expand(Q, H, 64).contiguous().cuda()
+    w = torch.zeros(S)     # K_p value of each selected position
+    vv = torch.ones(S)     # K_c (= V) value
+    for s0 in range(0, S, 128):  # 4 splits of 4 tiles
+        w[s0 + 32], vv[s0 + 32] = 2.5, -1.0   # tile 1: +9.6
+        w[s0 + 96], vv[s0 + 96] = 5.0, -1.0   # tile 3: +19.2
+    phys = torch.from_numpy(orc.dsa_translate(logical.cpu().numpy(), pt.cpu().numpy(), page)
+                            .astype(np.int64)).cuda()          # [Q, S]
+    rows = torch.empty((Q, S, 576), dtype=torch.float32)
+    rows[:, :, :512] = vv[None, :, None]
+    rows[:, :, 512:] = w[None, :, None]
+    cache.index_copy_(0, phys.reshape(-1), rows.reshape(-1, 576).to(torch.bfloat16).view(torch.int16).cuda())
+    err = _paged_case(amd, orc, Q, H, S, ctx, page=page, check_q=[0, 31, 63],
+                      inputs=(qn, qp, cache, pt, logical, pps))
+    assert err < 1e-2
