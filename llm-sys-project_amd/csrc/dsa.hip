@@ -676,21 +676,50 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
     const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
     const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,
-    float* __restrict__ part_ml, int H,
+    float* __restrict__ part_ml, int Q, int H,
     int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int* s_rows = (int*)(smem + kRows32Off);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // work item lin = (query, head group, split), dealt to the 8 XCDs in
+    // contiguous chunks (workgroup b runs on XCD b % 8): the splits of a
+    // query share an XCD, so its q rows come from HBM once and its partials
+    // are written and merged within one L2
     const int hgroups = H / 128;
-    const int sp = blockIdx.x % nsplit;
-    const int qh = blockIdx.x / nsplit;
+    const int per = gridDim.x / 8;
+    const int lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int sp = lin % nsplit;
+    const int qh = lin / nsplit;
     const int hg = qh % hgroups, qi = qh / hgroups;
+    if (qi >= Q) return;  // padding of the grid to a multiple of 8
     const int t0 = sp * chunk;
     const int len = max(0, min(S, t0 + chunk) - t0);
     const int g = lane >> 4, c16 = lane & 15;
     const int hbase = 128 * hg + 32 * wave;  // this wave's first head
 
+    // Prologue, ordered so the q loads overlap the two dependent loads of
+    // the page-table translation: logical indices, then page-table entries,
+    // then q (36 loads per lane), then wait for all but the q loads.  The
+    // q loads are waited for (by the compiler) at tile 0's first S step.
+    // An index outside the sequence gives row -1: a zero row.
+    constexpr int kRowsPer = kMaxChunk / 256;
+    int li[kRowsPer], pg[kRowsPer];
+    {
+        const int* lg = logical + (size_t)qi * S + t0;
+        const int* pt = page_table + (size_t)qi * pages_per_seq;
+        const long seq = (long)pages_per_seq * page;
+#pragma unroll
+        for (int k = 0; k < kRowsPer; k++) li[k] = tid + 256 * k < len ? lg[tid + 256 * k] : -1;
+#pragma unroll
+        for (int k = 0; k < kRowsPer; k++) {
+            const bool ok = li[k] >= 0 && li[k] < seq;
+            if (!ok) li[k] = -1;
+            pg[k] = ok ? pt[li[k] / page] : 0;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // q of heads hbase + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
     u32x4 qf[2][18];
 #pragma unroll
     for (int ht = 0; ht < 2; ht++) {
@@ -702,19 +731,12 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) qf[ht][16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
     }
-    // page-table translation of the split's logical indices (an index
-    // outside the sequence gives row -1: a zero row)
-    {
-        const int* lg = logical + (size_t)qi * S + t0;
-        const int* pt = page_table + (size_t)qi * pages_per_seq;
-        const long seq = (long)pages_per_seq * page;
-        for (int i = tid; i < len; i += 256) {
-            const int li = lg[i];
-            s_rows[i] = (li >= 0 && li < seq) ? pt[li / page] * page + li % page : -1;
-        }
-    }
-    // q of heads hbase + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
-    __syncthreads();  // s_rows visible; regular loads complete
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<36>();  // every page-table entry has arrived
+#pragma unroll
+    for (int k = 0; k < kRowsPer; k++)
+        if (tid + 256 * k < len) s_rows[tid + 256 * k] = li[k] >= 0 ? pg[k] * page + li[k] % page : -1;
+    lds_barrier();  // s_rows visible (the q loads stay in flight)
 
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
     // DMA: block b of a tile is filled by one instruction, lane l taking
@@ -920,10 +942,15 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
 // is 1 KB contiguous, and lane (g, c) holds dims 16mt + 4g + i of head c.
 __global__ __launch_bounds__(256) void dsa_merge_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_ml,
-                                                        uint16_t* __restrict__ out, int H,
-                                                        int nsplit) {
+                                                        uint16_t* __restrict__ out, int Q,
+                                                        int H, int nsplit) {
+    // same XCD dealing as dsa_split_kernel: a query's blocks on the XCD
+    // whose L2 holds its partials
     const int h16 = H / 16;
-    const int qi = blockIdx.x / h16, hb = blockIdx.x % h16;
+    const int per = gridDim.x / 8;
+    const int lin = (blockIdx.x % 8) * per + blockIdx.x / 8;
+    const int qi = lin / h16, hb = lin % h16;
+    if (qi >= Q) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int h = 16 * hb + c16;
@@ -985,7 +1012,7 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
         const size_t need = dsa_paged_scratch_bytes(Q, H, S);
         AMDMOE_CHECK_ARG(scratch != nullptr && scratch_bytes >= need,
                          "dsa_decode_bf16_paged: scratch of %zu bytes, %zu needed", scratch_bytes, need);
-        const long grid = (long)Q * (H / 128) * ns;
+        const long grid = ceil_div((long)Q * (H / 128) * ns, 8) * 8;
         AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_decode_bf16_paged: grid too large");
         static bool attr_split = false;
         if (!attr_split) {
@@ -999,10 +1026,10 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
         float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes);
         hipLaunchKernelGGL(dsa_split_kernel, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
                            qp, cache, cache_tokens * kRowBytes, page_table, logical, part_o, spare_o,
-                           part_ml, H, S, page, pages_per_seq, ns, chunk, scale_log2);
+                           part_ml, Q, H, S, page, pages_per_seq, ns, chunk, scale_log2);
         AMDMOE_LAUNCH_CHECK();
-        hipLaunchKernelGGL(dsa_merge_kernel, dim3((unsigned)((long)Q * (H / 16))), dim3(256), 0, st,
-                           (const float*)part_o, (const float*)part_ml, out, H, ns);
+        hipLaunchKernelGGL(dsa_merge_kernel, dim3((unsigned)(ceil_div((long)Q * (H / 16), 8) * 8)),
+                           dim3(256), 0, st, (const float*)part_o, (const float*)part_ml, out, Q, H, ns);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
     }
