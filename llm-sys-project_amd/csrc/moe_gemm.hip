@@ -117,7 +117,9 @@ __device__ __forceinline__ u32x4 hi4(const i32x8& x) {
     return (u32x4){(uint32_t)x[4], (uint32_t)x[5], (uint32_t)x[6], (uint32_t)x[7]};
 }
 
-template <int DT, int MODE>
+// PK: weights in fragment-block order (pack_weights), a separate
+// instantiation so the two layouts are distinct kernels
+template <int DT, int MODE, bool PK>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int ES = DtTraits<DT>::es;
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // row-major: lane (q, r16) reads row n at K offset 16q (+64 for the
         // hi half); fragment blocks: the 16 rows' 2 KB K-step is stored as
         // [half][lane][16 B], so each load is 1 KB contiguous
-        const long nb = g.b_packed ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
+        const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
         voff_b[ct] = ok ? (uint32_t)nb : kOob;
     }
     // DOWN: the flat slot and routing weight of each of the tile's rows ->
@@ -252,8 +254,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const int kb = kblk(kt_b);
             const int ct = (sl - kASlots) >> 1;
             const uint32_t vo = live ? voff_b[ct] : kOob;
-            const int sstep = g.b_packed ? kb * 2048 : kb * 128;
-            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (g.b_packed ? 1024 : 64));
+            const int sstep = PK ? kb * 2048 : kb * 128;
+            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (PK ? 1024 : 64));
             else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
         }
     };
@@ -581,11 +583,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
 // Upper bound of M-tiles for P routed rows over E experts.
 long max_mtiles(long P, int E) { return P / kBM + (P < E ? P : E); }
 
-template <int DT, int MODE>
+template <int DT, int MODE, bool PK>
 static int launch_one(const GemmArgs& g, long max_tiles, hipStream_t st) {
     static bool attr_set = false;
     if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)grouped_gemm_kernel<DT, MODE>,
+        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)grouped_gemm_kernel<DT, MODE, PK>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds));
         attr_set = true;
     }
@@ -593,7 +595,7 @@ static int launch_one(const GemmArgs& g, long max_tiles, hipStream_t st) {
     long grid = 8 * ceil_div(work, 8);
     if (grid == 0) return AMDMOE_OK;
     AMDMOE_CHECK_ARG(grid < (1L << 31), "grouped gemm: grid too large (%ld)", grid);
-    hipLaunchKernelGGL((grouped_gemm_kernel<DT, MODE>), dim3((unsigned)grid), dim3(512), kGemmLds,
+    hipLaunchKernelGGL((grouped_gemm_kernel<DT, MODE, PK>), dim3((unsigned)grid), dim3(512), kGemmLds,
                        st, g);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
@@ -607,12 +609,15 @@ int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hip
                      "grouped gemm: an operand exceeds 4 GiB (A %ld, expert %ld bytes)", g.a_bytes,
                      g.b_expert_bytes);
     AMDMOE_CHECK_ARG(dt != DT_FP8 || g.K / 128 <= kMaxKb, "grouped gemm: K=%d too large for fp8", g.K);
-    if (dt == DT_F32) return mode == MODE_UP ? launch_one<DT_F32, MODE_UP>(g, max_tiles, st)
-                                             : launch_one<DT_F32, MODE_DOWN>(g, max_tiles, st);
-    if (dt == DT_BF16) return mode == MODE_UP ? launch_one<DT_BF16, MODE_UP>(g, max_tiles, st)
-                                              : launch_one<DT_BF16, MODE_DOWN>(g, max_tiles, st);
-    return mode == MODE_UP ? launch_one<DT_FP8, MODE_UP>(g, max_tiles, st)
-                           : launch_one<DT_FP8, MODE_DOWN>(g, max_tiles, st);
+    AMDMOE_CHECK_ARG(!g.b_packed || dt == DT_FP8, "grouped gemm: packed weights are fp8 only");
+    if (dt == DT_F32) return mode == MODE_UP ? launch_one<DT_F32, MODE_UP, false>(g, max_tiles, st)
+                                             : launch_one<DT_F32, MODE_DOWN, false>(g, max_tiles, st);
+    if (dt == DT_BF16) return mode == MODE_UP ? launch_one<DT_BF16, MODE_UP, false>(g, max_tiles, st)
+                                              : launch_one<DT_BF16, MODE_DOWN, false>(g, max_tiles, st);
+    if (g.b_packed) return mode == MODE_UP ? launch_one<DT_FP8, MODE_UP, true>(g, max_tiles, st)
+                                           : launch_one<DT_FP8, MODE_DOWN, true>(g, max_tiles, st);
+    return mode == MODE_UP ? launch_one<DT_FP8, MODE_UP, false>(g, max_tiles, st)
+                           : launch_one<DT_FP8, MODE_DOWN, false>(g, max_tiles, st);
 }
 
 }  // namespace amdmoe
