@@ -10,32 +10,67 @@
 
 namespace amdmoe {
 
-// One wave per (row, 128-column block); each lane converts 2 values.
+// max over the 16 lanes of a DPP row (xor 1, xor 2, half-row mirror, row
+// mirror): every lane of the row ends with the row's maximum
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                                CTRL, 0xF, 0xF, false)));
+}
+
+// One wave per row.  A 128-column block is one 16-lane row of the wave
+// (8 values = 16 bytes per lane), so a wave step covers 4 blocks and the
+// block amax is a DPP reduction within the row; 8 steps (64 KB per CU) are
+// loaded before any is converted.
+constexpr int kQrBatch = 8;
+
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x, long rows,
                                                          int cols, uint8_t* __restrict__ q,
                                                          float* __restrict__ scale) {
-    const int nb = cols / 128;
-    const long job = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (job >= rows * nb) return;
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;  // whole wave
     const int lane = threadIdx.x & 63;
-    const long r = job / nb;
-    const int b = (int)(job % nb);
-    const size_t off = (size_t)r * cols + (size_t)b * 128 + lane * 2;
-    uint32_t pair = *(const uint32_t*)(x + off);
-    float v0 = bf16_to_f32((uint16_t)(pair & 0xffff)), v1 = bf16_to_f32((uint16_t)(pair >> 16));
-    float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-    float s = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 1.0f;
-    uint32_t c = f32x4_to_e4m3x4(__fdiv_rn(v0, s), __fdiv_rn(v1, s), 0.0f, 0.0f);
-    *(uint16_t*)(q + off) = (uint16_t)(c & 0xffff);
-    if (lane == 0) scale[r * nb + b] = s;
+    const int nb = cols / 128;
+    const int nsteps = (nb + 3) / 4;
+    const uint16_t* xr = x + (size_t)r * cols;
+    uint8_t* qr = q + (size_t)r * cols;
+    for (int s0 = 0; s0 < nsteps; s0 += kQrBatch) {
+        u32x4 v[kQrBatch];
+#pragma unroll
+        for (int i = 0; i < kQrBatch; i++) {
+            const int col = (s0 + i) * 512 + 8 * lane;
+            v[i] = col < cols ? *(const u32x4*)(xr + col) : (u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < kQrBatch; i++) {
+            const int col = (s0 + i) * 512 + 8 * lane;
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                f[2 * k] = __uint_as_float(v[i][k] << 16);
+                f[2 * k + 1] = __uint_as_float(v[i][k] & 0xffff0000u);
+            }
+            float am = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(f[k]));
+            am = dpp_max<0x140>(dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(am))));
+            if (col >= cols) continue;  // the whole 16-lane block is past the row
+            const float sc = am > 0.0f ? __fdiv_rn(am, 448.0f) : 1.0f;
+            u32x2 c;
+            c[0] = f32x4_to_e4m3x4(__fdiv_rn(f[0], sc), __fdiv_rn(f[1], sc), __fdiv_rn(f[2], sc), __fdiv_rn(f[3], sc));
+            c[1] = f32x4_to_e4m3x4(__fdiv_rn(f[4], sc), __fdiv_rn(f[5], sc), __fdiv_rn(f[6], sc), __fdiv_rn(f[7], sc));
+            *(u32x2*)(qr + col) = c;
+            if ((lane & 15) == 0) scale[r * nb + col / 128] = sc;
+        }
+    }
 }
 
 int launch_quant_rows(const uint16_t* x, long rows, int cols, uint8_t* q, float* scale,
                       hipStream_t st) {
     AMDMOE_CHECK_ARG(cols % 128 == 0 && cols > 0, "quant_rows: cols=%d not a multiple of 128", cols);
-    long jobs = rows * (cols / 128);
-    if (jobs == 0) return AMDMOE_OK;
-    hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)ceil_div(jobs, 4)), dim3(256), 0, st, x,
+    if (rows == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(ceil_div(rows, 4) < (1L << 31), "quant_rows: %ld rows", rows);
+    hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, x,
                        rows, cols, q, scale);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;

@@ -40,17 +40,18 @@ def announce(msg):
 
 
 # ------------------------------------------------------------------ formats
-def test_quant_rows_bit_exact(amd, orc):
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((37, 512)).astype(np.float32) * np.float32(3.0)
+@pytest.mark.parametrize("cols", [512, 128, 640, 7168])
+def test_quant_rows_bit_exact(amd, orc, cols):
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((37, cols)).astype(np.float32) * np.float32(3.0)
     x[3, :128] = 0.0
-    x[5, 128:256] *= np.float32(1e-5)                     # subnormal e4m3 codes
-    x[7, 256:384] = np.float32(1.0)                       # constant block
+    x[5, -128:] *= np.float32(1e-5)                       # subnormal e4m3 codes
+    x[7, cols // 256 * 128:][:128] = np.float32(1.0)      # constant block
     xb = orc.f32_to_bf16(x)
     xf = orc.bf16_to_f32(xb)
     q_ref, s_ref = orc.quant_rows_1x128(xf)
-    q = torch.empty((37, 512), dtype=torch.uint8, device="cuda")
-    s = torch.empty((37, 4), dtype=torch.float32, device="cuda")
+    q = torch.empty((37, cols), dtype=torch.uint8, device="cuda")
+    s = torch.empty((37, cols // 128), dtype=torch.float32, device="cuda")
     amd.quant_rows_fp8(dev(xb), q, s)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(s), s_ref)
