@@ -76,6 +76,77 @@ __global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypa
     }
 }
 
+// bf16 form for K <= 64: the slot order is computed in parallel (lane k of
+// wave 0: is slot k the first occurrence of a valid expert, and its rank
+// among the kept slots by expert id), and each thread loads all of its rows
+// (8 at a time, 4 column groups each) before adding them in that order, so
+// 32 loads per thread are in flight.
+__global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __restrict__ ypair,
+                                                           const int* __restrict__ idx, int T,
+                                                           int K, int E, int D,
+                                                           uint16_t* __restrict__ y) {
+    __shared__ int s_ord[64];
+    __shared__ int s_n;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid < 64) {
+        const int e = tid < K ? idx[(size_t)t * K + tid] : -1;
+        const bool valid = e >= 0 && e < E;
+        bool dup = false;
+        for (int j = 0; j < K; j++) {
+            const int ej = __shfl(e, j, kWave);
+            dup |= j < tid && ej == e;
+        }
+        const bool kept = valid && !dup;
+        const unsigned long long kb = __ballot(kept);
+        int rank = 0;
+        for (int j = 0; j < K; j++) {
+            const int ej = __shfl(e, j, kWave);
+            rank += ((kb >> j) & 1) && ej < e;
+        }
+        if (kept) s_ord[rank] = tid;
+        if (tid == 0) s_n = __popcll(kb);
+    }
+    __syncthreads();
+    const int n = s_n;
+    const int ng = D / 8;  // 8-column groups
+    constexpr int kG = 4, kR = 8;
+    f32x4 acc[kG][2];
+#pragma unroll
+    for (int i = 0; i < kG; i++) acc[i][0] = acc[i][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < n; j0 += kR) {
+        u32x4 v[kR][kG];
+#pragma unroll
+        for (int j = 0; j < kR; j++) {
+            const int jj = j0 + j;
+            const uint16_t* row = ypair + ((size_t)t * K + s_ord[jj < n ? jj : 0]) * D;
+#pragma unroll
+            for (int i = 0; i < kG; i++) {
+                const int c = tid + 256 * i;
+                v[j][i] = (jj < n && c < ng) ? *(const u32x4*)(row + 8 * c) : (u32x4){0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kR; j++) {
+            if (j0 + j >= n) break;  // uniform
+#pragma unroll
+            for (int i = 0; i < kG; i++)
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    acc[i][m >> 1][2 * (m & 1)] += __uint_as_float(v[j][i][m] << 16);
+                    acc[i][m >> 1][2 * (m & 1) + 1] += __uint_as_float(v[j][i][m] & 0xffff0000u);
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kG; i++) {
+        const int c = tid + 256 * i;
+        if (c >= ng) break;
+        u32x4 o;
+        for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(acc[i][m >> 1][2 * (m & 1)], acc[i][m >> 1][2 * (m & 1) + 1]);
+        *(u32x4*)(y + (size_t)t * D + 8 * c) = o;
+    }
+}
+
 int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,
                    hipStream_t st) {
     AMDMOE_CHECK_ARG(K <= 64 && D % 8 == 0, "combine: K=%d D=%d unsupported", K, D);
@@ -83,6 +154,9 @@ int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int 
     if (dt == DT_F32)
         hipLaunchKernelGGL((combine_kernel<float, false>), dim3(T), dim3(256), 0, st,
                            (const float*)ypair, idx, T, K, E, D, y);
+    else if (D <= 8 * 256 * 4)
+        hipLaunchKernelGGL(combine_bf16_kernel, dim3(T), dim3(256), 0, st, (const uint16_t*)ypair,
+                           idx, T, K, E, D, (uint16_t*)y);
     else
         hipLaunchKernelGGL((combine_kernel<uint16_t, true>), dim3(T), dim3(256), 0, st,
                            (const uint16_t*)ypair, idx, T, K, E, D, y);
