@@ -62,6 +62,7 @@ constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [
 constexpr int kGemmLds = kRowInfoOff + kBM * 8;           // 107520
 static_assert(kEpiRows * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
 static_assert(kBM == 256, "the wave layout assumes 256-row tiles");
+static_assert(128 * 544 <= kNS * kStageBytes, "DOWN epilogue staging fits the ring");
 
 template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
@@ -550,29 +551,61 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
         }
     } else {
-        // Stored straight from the accumulators: lane (q, r16) holds output
-        // columns n0 + 4q .. +3 of token row 16 rt + r16, so each row's 512
-        // bytes are written as 8-byte (bf16) or 16-byte (fp32) pieces; the
-        // row's slot and routing weight come from LDS.
+        // lane (q, r16) holds output columns n0 + 32w + 16ct + 4q .. +3 of
+        // token row 16 rt + r16; the row's slot and routing weight come from
+        // LDS (staged in the prologue)
         const int* s_slot = (const int*)(smem + kRowInfoOff);
         const float* s_wt = (const float*)(smem + kRowInfoOff) + kBM;
+        if (DT == DT_F32) {
+            // fp32 (the reference path): 16-byte stores straight from the accumulators
 #pragma unroll
-        for (int rt = 0; rt < 16; rt++) {
-            if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
-            const int r = 16 * rt + r16;
-            if (r >= rows) continue;
-            const size_t sl = (size_t)s_slot[r];
-            const float wgt = s_wt[r];
+            for (int rt = 0; rt < 16; rt++) {
+                if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
+                const int r = 16 * rt + r16;
+                if (r >= rows) continue;
+                const size_t sl = (size_t)s_slot[r];
+                const float wgt = s_wt[r];
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
-                const int n = nt * 256 + 32 * wave + 16 * ct + 4 * q;
-                if (n >= g.n_out) continue;
-                const f32x4 v = acc[rt][ct] * wgt;
-                if (DT == DT_F32) {
-                    *(f32x4*)((float*)g.out + sl * g.n_out + n) = v;
-                } else {
-                    const u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                    *(u32x2*)(g.out + (sl * g.n_out + n) * 2) = pk;
+                for (int ct = 0; ct < 2; ct++) {
+                    const int n = nt * 256 + 32 * wave + 16 * ct + 4 * q;
+                    if (n >= g.n_out) continue;
+                    *(f32x4*)((float*)g.out + sl * g.n_out + n) = acc[rt][ct] * wgt;
+                }
+            }
+        } else {
+            // bf16: the weighted rows are staged through the (now idle) ring,
+            // 128 rows per pass as bf16 with a 544-byte pitch (16 rows of a
+            // 32-byte piece hit each bank at most twice), then every thread
+            // stores 16 contiguous bytes: one instruction writes two full
+            // 512-byte row segments instead of 16 rows x 32 bytes
+            constexpr int kPitch = 544;
+            uint8_t* stg = smem;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                if (128 * half >= rows) continue;  // uniform
+                if (half) __syncthreads();          // pass 0's reads are done
+#pragma unroll
+                for (int r8 = 0; r8 < 8; r8++) {
+                    const int rt = 8 * half + r8;
+                    const float wgt = s_wt[16 * rt + r16];
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++) {
+                        const f32x4 v = acc[rt][ct] * wgt;
+                        *(u32x2*)(stg + (16 * r8 + r16) * kPitch + (32 * wave + 16 * ct + 4 * q) * 2) =
+                            (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
+                }
+                lds_barrier();
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int c = tid + 512 * j;       // 16-byte chunk of the pass
+                    const int rr = c >> 5, ch = c & 31;  // row in the pass, chunk in the row
+                    const int r = 128 * half + rr;
+                    const int n = nt * 256 + 8 * ch;
+                    if (r < rows && n < g.n_out) {
+                        const u32x4 v = *(const u32x4*)(stg + rr * kPitch + 16 * ch);
+                        *(u32x4*)(g.out + ((size_t)s_slot[r] * g.n_out + n) * 2) = v;
+                    }
                 }
             }
         }
