@@ -43,6 +43,7 @@ struct MoeWs {
     int4* tiles;
     int* sorted_token;
     int* sorted_slot;
+    float* sorted_w;
     uint8_t* xq;
     float* xs;
     uint8_t* act;
@@ -75,6 +76,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     w.tiles = (int4*)take(16 * (size_t)max_mtiles((long)P, (int)E));
     w.sorted_token = (int*)take(4 * P);
     w.sorted_slot = (int*)take(4 * P);
+    w.sorted_w = (float*)take(4 * P);
     w.perm = (int*)take(permute_scratch_bytes((int)T, (int)E));
     if (dtype == AMDMOE_DTYPE_FP8) {
         w.xq = take(T * D);
@@ -167,7 +169,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);
     TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
                        w.sorted_slot, w.tiles, w.num_tiles,
-                       permute_scratch_bytes(T, E) ? w.perm : nullptr, st));
+                       permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st));
     TRY(mark(3, st));
     GemmArgs up{};
     up.a = a_x;
@@ -210,7 +212,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.n_tiles_n = (int)ceil_div(D, 256);
     dn.out = w.ypair;
     dn.sorted_slot = w.sorted_slot;
-    dn.wts = w.wts;
+    dn.sorted_w = w.sorted_w;
     TRY(launch_grouped_gemm(dt, MODE_DOWN, dn, mtiles, st));
     TRY(mark(5, st));
     TRY(launch_combine(dt == DT_F32 ? DT_F32 : DT_BF16, w.ypair, w.idx, T, K, E, D, y, st));
@@ -394,7 +396,8 @@ int amdmoe_moe_permute(const int* expert_indices, const MoeConfig* cfg, int* cou
     int* nt = (int*)((uint8_t*)scratch + tiles_bytes);
     int* perm = perm_bytes ? (int*)((uint8_t*)scratch + tiles_bytes + 256) : nullptr;
     return launch_permute(expert_indices, c.num_tokens, c.top_k, c.num_experts, kMTile, counts,
-                          offsets, sorted_token, sorted_slot, tiles, nt, perm, (hipStream_t)stream);
+                          offsets, sorted_token, sorted_slot, tiles, nt, perm, nullptr, nullptr,
+                          (hipStream_t)stream);
 }
 
 int amdmoe_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,

@@ -32,7 +32,7 @@ struct GemmArgs {
     uint8_t* out;            // UP: act [P, I]; DOWN: ypair [T*K, D]
     float* out_scale;        // UP fp8: act scales [P, I/128]
     const int* sorted_slot;  // DOWN: flat slot t*K+k of each sorted row
-    const float* wts;        // DOWN: routing weights [T*K]
+    const float* sorted_w;   // DOWN: routing weight of each sorted row
 };
 
 // moe_route.hip
@@ -49,9 +49,10 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
 // scratch: permute_scratch_bytes(T, E) bytes, or nullptr (single-launch
 // kernel); permute_scratch_bytes returns 0 where only the latter applies
 size_t permute_scratch_bytes(int T, int E);
+// wts / sorted_w: optional (both or neither): sorted_w[row] = wts[slot of row]
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   int* scratch, hipStream_t st);
+                   int* scratch, const float* wts, float* sorted_w, hipStream_t st);
 int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D, int expert,
                       float* gathered, int* token_map, int* count, hipStream_t st);
 

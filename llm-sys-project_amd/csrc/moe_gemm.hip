@@ -157,22 +157,43 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // ---- activation DMA offsets: wave w fills rows [32w, 32w+32) ----
     const int lrow = lane >> 3;              // row within an 8-row, 1 KB slab
     const int lchunk = (lane & 7) ^ lrow;    // global chunk landing at lane's LDS slot
+    // Prologue loads, issued together so they cost one round trip: the
+    // weight scales of this work item for every K block (fp8; one per
+    // thread, 2 * kb_per_row <= 256 of them, -> LDS before the main loop),
+    // UP's row indices (a_map), and DOWN's slot and routing weight of each
+    // row, which only the epilogue needs: those stay in flight through the
+    // main loop (the barrier below waits for the LDS writes, not for them).
+    // The loads are unconditional, from clamped in-range addresses: in a
+    // branch, each would be waited for on its own.
+    float sb_val = 0.0f;
+    int sb_pos = -1;
+    if (DT == DT_FP8) {
+        const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
+        const int i = min(tid, 2 * kb_per_row - 1);
+        const int which = i / kb_per_row, kb = i - which * kb_per_row;
+        const int nb = MODE == MODE_UP ? (which == 0 ? nt : g.n_out / 128 + nt)
+                                       : min(2 * nt + which, g.b_rows / 128 - 1);
+        sb_val = bse[(size_t)nb * kb_per_row + kb];
+        sb_pos = tid < 2 * kb_per_row ? which * kMaxKb + kb : -1;
+    }
+    // UP gathers the rows through a_map (index clamped to a live row; the
+    // offset of a row past the tile is replaced by the out-of-range one)
+    long arow[5];
+#pragma unroll
+    for (int j = 0; j < 5; j++) {
+        const int r = j < 4 ? 32 * wave + 8 * j + lrow : 32 * wave + (lane & 31);
+        arow[j] = MODE == MODE_UP ? (long)g.a_map[row0 + min(r, rows - 1)] : (long)(row0 + r);
+    }
     uint32_t voff_a[4];
+#pragma unroll
     for (int j = 0; j < 4; j++) {
         const int r = 32 * wave + 8 * j + lrow;
-        voff_a[j] = kOob;
-        if (r < rows) {
-            const long ar = MODE == MODE_UP ? (long)g.a_map[row0 + r] : (long)(row0 + r);
-            voff_a[j] = (uint32_t)(ar * g.a_row_bytes + 16 * lchunk);
-        }
+        voff_a[j] = r < rows ? (uint32_t)(arow[j] * g.a_row_bytes + 16 * lchunk) : kOob;
     }
     uint32_t voff_s = kOob;
     if (DT == DT_FP8) {
         const int r = 32 * wave + lane;
-        if (lane < 32 && r < rows) {
-            const long ar = MODE == MODE_UP ? (long)g.a_map[row0 + r] : (long)(row0 + r);
-            voff_s = (uint32_t)(ar * kb_per_row * 4);
-        }
+        if (lane < 32 && r < rows) voff_s = (uint32_t)(arow[4] * kb_per_row * 4);
     }
 
     // ---- weight rows of this wave: two MFMA column tiles of 16 ----
@@ -197,26 +218,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
         voff_b[ct] = ok ? (uint32_t)nb : kOob;
     }
-    // DOWN: the flat slot and routing weight of each of the tile's rows ->
-    // LDS (two dependent gathers, overlapped with the scale loads below and
-    // waited for by the barrier before the main loop)
+    __builtin_amdgcn_sched_barrier(0);
     int row_slot = 0;
-    if (MODE == MODE_DOWN && tid < rows) row_slot = g.sorted_slot[(size_t)row0 + tid];
-    if (DT == DT_FP8) {
-        // weight scales of this work item for every K block -> LDS
-        float* sbs = (float*)(smem + kBScaleOff);
-        const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
-        for (int i = tid; i < 2 * kb_per_row; i += 512) {
-            const int which = i / kb_per_row, kb = i - which * kb_per_row;
-            const int nb = MODE == MODE_UP ? (which == 0 ? nt : g.n_out / 128 + nt)
-                                           : min(2 * nt + which, g.b_rows / 128 - 1);
-            sbs[which * kMaxKb + kb] = bse[(size_t)nb * kb_per_row + kb];
-        }
+    float row_w = 0.0f;
+    if (MODE == MODE_DOWN) {
+        const size_t r = (size_t)row0 + min(tid, rows - 1);  // rows >= 1
+        row_slot = g.sorted_slot[r];
+        row_w = tid < rows ? g.sorted_w[r] : 0.0f;
     }
-    if (MODE == MODE_DOWN && tid < kBM) {
-        ((int*)(smem + kRowInfoOff))[tid] = row_slot;
-        ((float*)(smem + kRowInfoOff))[kBM + tid] = tid < rows ? g.wts[row_slot] : 0.0f;
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (sb_pos >= 0) ((float*)(smem + kBScaleOff))[sb_pos] = sb_val;
 
     // K-steps run in a rotated order starting at kt0, keyed by the M-tile:
     // the N-tiles of one M-tile run together on one XCD and read the same
@@ -397,7 +408,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         }
     };
 
-    __syncthreads();  // weight scales in LDS; every regular load has completed
+    static_assert(2 * kMaxKb <= 512, "one weight-scale load per thread");
+    lds_barrier();  // weight scales in LDS (DOWN's slot / weight loads may still be in flight)
     // Prefetch distances: activations 2 K-steps ahead (a 3-stage LDS ring;
     // they come from L2), weights RB-1 K-steps ahead in a ring of RB
     // register sets -- as deep as the registers left by the live
@@ -477,7 +489,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         case 3: main_loop(std::integral_constant<int, 3>()); break;
         default: main_loop(std::integral_constant<int, 4>()); break;
     }
-    __syncthreads();  // every wave is done with the ring before it is reused
+    if (MODE == MODE_DOWN && tid < kBM) {
+        ((int*)(smem + kRowInfoOff))[tid] = row_slot;
+        ((float*)(smem + kRowInfoOff))[kBM + tid] = row_w;
+    }
+    __syncthreads();  // every wave is done with the ring before it is reused; row info in LDS
 
     // ---- epilogues (LDS staging for coalesced 16-byte stores), 128 rows
     //      per pass; every wave holds all rows of its columns ----

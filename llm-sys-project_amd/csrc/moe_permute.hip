@@ -46,7 +46,8 @@ __device__ __forceinline__ int token_slot_of(const int* __restrict__ row, int K,
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     const int* __restrict__ idx, int T, int K, int E, int BM, int* __restrict__ counts,
     int* __restrict__ offsets, int* __restrict__ sorted_token, int* __restrict__ sorted_slot,
-    int4* __restrict__ tiles, int* __restrict__ num_tiles) {
+    int4* __restrict__ tiles, int* __restrict__ num_tiles, const float* __restrict__ wts,
+    float* __restrict__ sorted_w) {
     extern __shared__ int s_hist[];            // [E]
     __shared__ int s_wave[kPermThreads / 64];  // per-wave totals
     __shared__ int s_red[2];
@@ -118,6 +119,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
             int pos = row_off + base + before + rank_in_wave;
             sorted_token[pos] = t;
             sorted_slot[pos] = t * K + k;
+            if (sorted_w) sorted_w[pos] = wts[(size_t)t * K + k];
         }
         base += total;
     }
@@ -242,7 +244,9 @@ __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int* __res
                                                                 int K, int E,
                                                                 const int* __restrict__ blk_off,
                                                                 int* __restrict__ sorted_token,
-                                                                int* __restrict__ sorted_slot) {
+                                                                int* __restrict__ sorted_slot,
+                                                                const float* __restrict__ wts,
+                                                                float* __restrict__ sorted_w) {
     extern __shared__ unsigned long long s_mask[];  // [E]
     perm_masks(idx, T, K, E, s_mask);
     const int lane = threadIdx.x;
@@ -259,6 +263,7 @@ __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int* __res
         const int pos = blk_off[(size_t)blockIdx.x * E + v] + __popcll(s_mask[v] & below);
         sorted_token[pos] = t;
         sorted_slot[pos] = t * K + k;
+        if (sorted_w) sorted_w[pos] = wts[(size_t)t * K + k];
     }
 }
 
@@ -270,7 +275,8 @@ size_t permute_scratch_bytes(int T, int E) {
 
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   int* scratch, hipStream_t st) {
+                   int* scratch, const float* wts, float* sorted_w, hipStream_t st) {
+    AMDMOE_CHECK_ARG((wts == nullptr) == (sorted_w == nullptr), "permute: wts and sorted_w go together");
     if (scratch && T > 0 && permute_scratch_bytes(T, E) > 0) {
         const int nblk = (T + kPermTok - 1) / kPermTok;
         int* blk_cnt = scratch;
@@ -282,14 +288,14 @@ int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int
                            counts, offsets, tiles, num_tiles);
         AMDMOE_LAUNCH_CHECK();
         hipLaunchKernelGGL(perm_scatter_kernel, dim3(nblk), dim3(kPermTok), lds, st, idx, T, K, E,
-                           blk_off, sorted_token, sorted_slot);
+                           blk_off, sorted_token, sorted_slot, wts, sorted_w);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
     }
     size_t lds = sizeof(int) * (size_t)E;
     AMDMOE_CHECK_ARG(lds <= 48 * 1024, "permute: E=%d too large", E);
     hipLaunchKernelGGL(permute_kernel, dim3(E), dim3(kPermThreads), lds, st, idx, T, K, E, BM,
-                       counts, offsets, sorted_token, sorted_slot, tiles, num_tiles);
+                       counts, offsets, sorted_token, sorted_slot, tiles, num_tiles, wts, sorted_w);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
