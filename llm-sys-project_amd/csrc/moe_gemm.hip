@@ -435,9 +435,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         //   RB == 3: the weights of step kt+1 (4), which follow the
         //            activations of step kt+1 (those are thus waited for
         //            one step early).
-        constexpr int kWait = RB == 5 ? 12 : 4;
-        static_assert(RB == 5 || RB == 3, "wait counts are derived for rings of 3 or 5 sets");
-        wait_vmcnt<kWait>();
+        //   RB == 4: the weights of steps kt+1, kt+2 (8) -- for a wave with
+        //            activation slots, whose step-kt activations precede
+        //            4 + kASlots + 4 later instructions, this also waits for
+        //            the first activation slot of step kt+1 (one count for
+        //            all waves: no path mixes the two).
+        static_assert(RB == 5 || RB == 4 || RB == 3, "wait counts are derived for rings of 3, 4 or 5 sets");
+        wait_vmcnt<RB == 5 ? 12 : (RB == 4 ? 8 : 4)>();
         // the weights of this step have landed: pin every use of them below
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
@@ -454,7 +458,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // sets are defined and consumed in one place with no moves between.
     auto main_loop = [&](auto ngc) __attribute__((always_inline)) {
         constexpr int NG = decltype(ngc)::value;
-        constexpr int RB = NG <= 3 ? 5 : 3;
+        constexpr int RB = NG <= 3 ? 4 : 3;
         const std::integral_constant<int, RB> rbc;
         const bool a_live = 32 * wave < 64 * NG;  // uniform
         // only the live token tiles' accumulators exist during the loop
