@@ -1,0 +1,665 @@
+// R3/R4/R5 -- single-launch grouped expert GEMMs on MFMA.
+//
+// Reference: the per-expert host loop of moe_forward
+// (kernels/moe/naive_moe.cu:424-470): per expert, GEMM1 [cnt,D]x[2I,D]^T
+// (tiled_gemm_bt_kernel, 246-280), swiglu_strided_kernel (297-310), GEMM2
+// [cnt,I]x[D,I]^T, then scatter_kernel (315-335) with the routing weight.
+//
+// Here each GEMM is ONE launch over every expert.  The permutation kernel
+// emits M-tiles {expert, first sorted row, rows} of up to 256 rows; a
+// workgroup owns one (M-tile, N-tile) work item:
+//   UP   (GEMM1 + SwiGLU): A rows are gathered straight from x through
+//        sorted_token (no permuted copy of x exists); the weight tile is 128
+//        gate rows n0.. and the 128 matching up rows I+n0.., so each wave has
+//        g and u of the same columns and writes act = silu(g)*u (fp8:
+//        requantised per 128 columns, the tile width).
+//   DOWN (GEMM2 + combine weight): A = act rows (contiguous, sorted order),
+//        256 rows of W2; the epilogue multiplies by the routing weight of the
+//        row's slot and writes the row to ypair[slot] (slot = t*K+k), from
+//        where the combine kernel sums each token's rows in ascending expert
+//        order -- the reference's scatter order, deterministic, no atomics.
+// fp8 block scales (128x128 weights, 1x128 activations): a K-step is exactly
+// one 128-wide K block, so each 16x16x128 MFMA yields a fresh partial that
+// is folded into the fp32 accumulator as acc += partial * (s_a[row]*s_w).
+//
+// Why the tile is 256 rows.  The layer is bound by streaming expert weights
+// from HBM.  With top-8 of 256 experts at T=4096 an expert sees 128 +- 11
+// tokens, so 128-row tiles split half the experts in two and those experts'
+// weights are streamed twice (measured: 1.7x the algorithmic bytes).  A
+// 256-row tile covers every expert at T <= ~7000 in one pass.
+//
+// Memory pipeline.  Activations: 256 rows x 128 bytes per K-step, global ->
+// LDS with buffer_load ... lds into a 3-stage ring (rows past the tile read
+// as zeros through the buffer descriptor); LDS rows are XOR-swizzled in
+// 16-byte chunks so 16-row fragment reads hit distinct banks.  Weights:
+// each of the 8 waves owns 32 weight rows and loads them straight into
+// registers in MFMA operand layout (a register ring of 4 K-step sets, 3 for
+// a full 16-tile M-tile), so the weight stream needs no LDS: three K-steps
+// (~96 KB per CU) are in flight while one is consumed.  Waits are explicit vmcnt counts and the barrier is a bare
+// s_barrier, so nothing drains mid-loop.
+//
+// Work items are laid out M-tile-major (all N-tiles of an M-tile are
+// consecutive) and dealt to XCDs in contiguous chunks (workgroup b runs on
+// XCD b % 8), so an M-tile's activation rows stay in one XCD's L2.
+//
+// The kernel template lives in this header; each moe_gemm_<type>.hip file
+// instantiates some of its variants (the fp8 ones are large: one main loop
+// per live token-tile count), so they compile in parallel.
+#pragma once
+
+#include <type_traits>
+#include <utility>
+
+#include "internal.hpp"
+
+namespace amdmoe {
+
+constexpr int kBM = kMTile;                            // 256
+constexpr int kNS = 3;                                 // ring stages (activations and weights)
+static_assert(kNS == 3, "activations are prefetched two K-steps ahead");
+constexpr int kATile = kBM * 128;                      // 32 KB
+constexpr int kSTile = 8 * 256;                        // A-scale slots, 256 B per wave
+constexpr int kStageBytes = kATile + kSTile;           // 34816
+constexpr int kBScaleOff = kNS * kStageBytes;          // fp8 weight scales [2][kMaxKb]
+constexpr int kMaxKb = 128;                            // K <= 16384 on the fp8 path
+constexpr int kEpiPitch = 132;                         // floats per staged output row
+constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
+constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
+constexpr int kGemmLds = kRowInfoOff + kBM * 8;           // 107520
+static_assert(kEpiRows * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
+static_assert(kBM == 256, "the wave layout assumes 256-row tiles");
+static_assert(128 * 544 <= kNS * kStageBytes, "DOWN epilogue staging fits the ring");
+
+template <int DT> struct DtTraits;
+template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
+template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
+template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
+
+// One K-step of a wave's weights in registers: per column tile the lane's
+// 32 bytes, lo 16 B at K offset 16q and hi 16 B at 64 + 16q (the fp8 MFMA
+// consumes them as one 8-dword tuple).
+struct BFrag {
+    u32x4 q[2][2];  // [column tile][lo, hi]
+};
+
+// An empty asm that reads and redefines the fragment: no use of it can move
+// above this point, and the compiler must assume its value changes here.
+__device__ __forceinline__ void pin(BFrag& f) {
+    asm volatile("" : "+v"(f.q[0][0]), "+v"(f.q[0][1]), "+v"(f.q[1][0]), "+v"(f.q[1][1]));
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte buffer load into registers, issued as inline asm so the compiler
+// does not insert its own vector-memory waits before the (much later) use;
+// the kernel's explicit vmcnt wait at the top of each K-step covers it.
+// OFF is the immediate offset; an out-of-range voffset reads zeros.
+// The buffer descriptor of make_rsrc() as four scalar words: base address,
+// stride 0, byte count, raw-buffer flags.
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, long bytes) {
+    const uint64_t p = (uint64_t)base;
+    return (i32x4){__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+                   __builtin_amdgcn_readfirstlane((int)((p >> 32) & 0xffff)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), kRsrcFlags};
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4 buffer_load_b128_async(i32x4 rsrc, uint32_t voff, int soff) {
+    u32x4 r;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4"
+                 : "=v"(r)
+                 : "v"(voff), "s"(rsrc), "s"(soff), "i"(OFF));
+    return r;
+}
+
+__device__ __forceinline__ i32x8 frag8(const BFrag& f, int ct) {
+    const u32x4 a = f.q[ct][0], b = f.q[ct][1];
+    return (i32x8){(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+}
+
+__device__ __forceinline__ u32x4 lo4(const i32x8& x) {
+    return (u32x4){(uint32_t)x[0], (uint32_t)x[1], (uint32_t)x[2], (uint32_t)x[3]};
+}
+__device__ __forceinline__ u32x4 hi4(const i32x8& x) {
+    return (u32x4){(uint32_t)x[4], (uint32_t)x[5], (uint32_t)x[6], (uint32_t)x[7]};
+}
+
+// PK: weights in fragment-block order (pack_weights), a separate
+// instantiation so the two layouts are distinct kernels
+template <int DT, int MODE, bool PK>
+__global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int ES = DtTraits<DT>::es;
+    // vector-memory instructions per K-step per wave ("slots"): 4
+    // activation slabs (+1 scale slot on fp8) into LDS, then 4 weight loads
+    // into registers; a wave whose activation rows are all past the live
+    // token tiles issues only the weight loads
+    constexpr int kASlots = 4 + (DT == DT_FP8 ? 1 : 0);
+    constexpr int kSlots = kASlots + 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+
+    // ---- work item (XCD-chunked) ----
+    const int W = (*g.num_tiles) * g.n_tiles_n;
+    const int per = (W + 7) >> 3;
+    const int slot = blockIdx.x >> 3;
+    if (slot >= per) return;
+    const int w = (blockIdx.x & 7) * per + slot;
+    if (w >= W) return;
+    const int mt = w / g.n_tiles_n, nt = w - mt * g.n_tiles_n;
+    const int4 tile = g.tiles[mt];
+    const int e = tile.x, row0 = tile.y, rows = tile.z;
+    const int nk = (int)((long)g.K * ES / 128);
+    const int kb_per_row = g.K / 128;  // fp8 scale blocks along K
+
+    // ---- buffer descriptors ----
+    const uint8_t* bexp = g.b + (size_t)e * g.b_expert_bytes;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
+    const i32x4 rb = make_rsrc_words(bexp, g.b_expert_bytes);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(DT == DT_FP8 ? (const void*)g.a_scale : (const void*)g.a,
+                  DT == DT_FP8 ? g.a_scale_bytes : 0);
+
+    // ---- activation DMA offsets: wave w fills rows [32w, 32w+32) ----
+    const int lrow = lane >> 3;              // row within an 8-row, 1 KB slab
+    const int lchunk = (lane & 7) ^ lrow;    // global chunk landing at lane's LDS slot
+    // Prologue loads, issued together so they cost one round trip: the
+    // weight scales of this work item for every K block (fp8; one per
+    // thread, 2 * kb_per_row <= 256 of them, -> LDS before the main loop),
+    // UP's row indices (a_map), and DOWN's slot and routing weight of each
+    // row, which only the epilogue needs: those stay in flight through the
+    // main loop (the barrier below waits for the LDS writes, not for them).
+    // The loads are unconditional, from clamped in-range addresses: in a
+    // branch, each would be waited for on its own.
+    float sb_val = 0.0f;
+    int sb_pos = -1;
+    if (DT == DT_FP8) {
+        const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
+        const int i = min(tid, 2 * kb_per_row - 1);
+        const int which = i / kb_per_row, kb = i - which * kb_per_row;
+        const int nb = MODE == MODE_UP ? (which == 0 ? nt : g.n_out / 128 + nt)
+                                       : min(2 * nt + which, g.b_rows / 128 - 1);
+        sb_val = bse[(size_t)nb * kb_per_row + kb];
+        sb_pos = tid < 2 * kb_per_row ? which * kMaxKb + kb : -1;
+    }
+    // UP gathers the rows through a_map (index clamped to a live row; the
+    // offset of a row past the tile is replaced by the out-of-range one)
+    long arow[5];
+#pragma unroll
+    for (int j = 0; j < 5; j++) {
+        const int r = j < 4 ? 32 * wave + 8 * j + lrow : 32 * wave + (lane & 31);
+        arow[j] = MODE == MODE_UP ? (long)g.a_map[row0 + min(r, rows - 1)] : (long)(row0 + r);
+    }
+    uint32_t voff_a[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = 32 * wave + 8 * j + lrow;
+        voff_a[j] = r < rows ? (uint32_t)(arow[j] * g.a_row_bytes + 16 * lchunk) : kOob;
+    }
+    uint32_t voff_s = kOob;
+    if (DT == DT_FP8) {
+        const int r = 32 * wave + lane;
+        if (lane < 32 && r < rows) voff_s = (uint32_t)(arow[4] * kb_per_row * 4);
+    }
+
+    // ---- weight rows of this wave: two MFMA column tiles of 16 ----
+    //   UP:   ct 0 = gate rows n0 + 16w + c, ct 1 = up rows I + n0 + 16w + c
+    //   DOWN: ct = rows n0 + 32w + 16ct + c
+    const int q = lane >> 4, r16 = lane & 15;
+    uint32_t voff_b[2];
+    for (int ct = 0; ct < 2; ct++) {
+        long n;
+        bool ok;
+        if (MODE == MODE_UP) {
+            const int col = nt * 128 + 16 * wave + r16;
+            ok = col < g.n_out;
+            n = ct == 0 ? col : (long)g.n_out + col;
+        } else {
+            n = (long)nt * 256 + 32 * wave + 16 * ct + r16;
+            ok = n < g.n_out;
+        }
+        // row-major: lane (q, r16) reads row n at K offset 16q (+64 for the
+        // hi half); fragment blocks: the 16 rows' 2 KB K-step is stored as
+        // [half][lane][16 B], so each load is 1 KB contiguous
+        const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
+        voff_b[ct] = ok ? (uint32_t)nb : kOob;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int row_slot = 0;
+    float row_w = 0.0f;
+    if (MODE == MODE_DOWN) {
+        const size_t r = (size_t)row0 + min(tid, rows - 1);  // rows >= 1
+        row_slot = g.sorted_slot[r];
+        row_w = tid < rows ? g.sorted_w[r] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (sb_pos >= 0) ((float*)(smem + kBScaleOff))[sb_pos] = sb_val;
+
+    // K-steps run in a rotated order starting at kt0, keyed by the M-tile:
+    // the N-tiles of one M-tile run together on one XCD and read the same
+    // activation K-slice at the same time (one fetch, the rest L2 hits),
+    // while different M-tiles start at different K offsets.
+    const int kt0 = (int)(((unsigned)mt * 7u) % (unsigned)nk);
+    auto kblk = [&](int kt) __attribute__((always_inline)) {
+        int k = kt + kt0;
+        k = k >= nk ? k - nk : k;
+        return k >= nk ? k - nk : k;
+    };
+
+    // Loads for a K-step past the end (kt >= nk) are still issued, with an
+    // out-of-range offset (they read zeros and touch no memory), so every
+    // step waits for the same vmcnt and no path through the loop skips a
+    // wait.  issue_slot(s, ...) issues one of the kSlots instructions of
+    // K-step kt into ring stage st / register set f.
+    // Activation slots load K-step kt_a into ring stage kt_a % kNS, weight
+    // slots load K-step kt_b into the register set f.
+    auto issue_slot = [&](int sl, bool a_live, int kt_a, int kt_b, BFrag& f) __attribute__((always_inline)) {
+        if (sl < kASlots) {
+            if (!a_live) return;
+            const bool live = kt_a < nk;
+            const int kb = kblk(kt_a);
+            uint8_t* stage = smem + (kt_a % kNS) * kStageBytes;
+            if (sl < 4)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (lds_ptr_t)(stage + (32 * wave + 8 * sl) * 128), 16,
+                    live ? voff_a[sl] : kOob, kb * 128, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (lds_ptr_t)(stage + kATile + wave * 256), 4,
+                    live ? voff_s : kOob, kb * 4, 0, 0);
+        } else {
+            const bool live = kt_b < nk;
+            const int kb = kblk(kt_b);
+            const int ct = (sl - kASlots) >> 1;
+            const uint32_t vo = live ? voff_b[ct] : kOob;
+            const int sstep = PK ? kb * 2048 : kb * 128;
+            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (PK ? 1024 : 64));
+            else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
+        }
+    };
+
+    const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
+
+    // acc[rt][ct] is the transposed output tile: lane (q, r16) holds weight
+    // columns 4q..4q+3 of column tile ct for token 16*rt + r16.
+    f32x4 acc[16][2];
+
+    // One K-step on ring stage ST with weights `bf`.  The MFMA computes
+    // C^T = W x^T: weights are operand A (rows = weight columns), tokens
+    // operand B, so each lane owns a single token and the activation block
+    // scale is one float per lane, while the weight block scale is uniform.
+    auto compute = [&](auto rc, const BFrag& bf, int kt, auto&& tile_issued) __attribute__((always_inline)) {
+        constexpr int R = decltype(rc)::value;
+        // the stage offset is made opaque so the compiler forms the LDS
+        // addresses here (one add, then immediate offsets) rather than
+        // hoisting one address register per stage and tile out of the loop
+        uint32_t soff_st = (kt % kNS) * kStageBytes;
+        asm volatile("" : "+s"(soff_st));
+        const uint8_t* base = smem + soff_st;
+        float sb0 = 0.f, sb1 = 0.f;
+        if (DT == DT_FP8) {
+            const float* sbs = (const float*)(smem + kBScaleOff);
+            const int kb = kblk(kt);
+            if (MODE == MODE_UP) { sb0 = sbs[kb]; sb1 = sbs[kMaxKb + kb]; }
+            else { sb0 = sb1 = sbs[(wave >> 2) * kMaxKb + kb]; }
+        }
+        auto load_x = [&](int rt, i32x8& xv, float& sx) __attribute__((always_inline)) {
+            const uint8_t* p = base + (16 * rt + r16) * 128;
+            const u32x4 lo = *(const u32x4*)(p + off_lo), hi = *(const u32x4*)(p + off_hi);
+            xv = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                         (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+            if (DT == DT_FP8) {
+                const int r = 16 * rt + r16;
+                sx = *(const float*)(base + kATile + (r >> 5) * 256 + (r & 31) * 4);
+            }
+        };
+        auto mma = [&](int rt, const i32x8& xv, float sx) __attribute__((always_inline)) {
+            const u32x4 xlo = lo4(xv), xhi = hi4(xv);
+            if (DT == DT_FP8) {
+                const float s0 = sx * sb0;
+                const float s1 = MODE == MODE_UP ? sx * sb1 : s0;
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const f32x4 pr = mfma_fp8(frag8(bf, ct), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
+                    const float sc = ct == 0 ? s0 : s1;
+                    for (int i = 0; i < 4; i++) acc[rt][ct][i] += pr[i] * sc;
+                }
+            } else {
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const u32x4 wlo = bf.q[ct][0], whi = bf.q[ct][1];
+                    if (DT == DT_F32) {
+                        for (int j = 0; j < 4; j++)
+                            acc[rt][ct] = mfma_f32(__uint_as_float(wlo[j]), __uint_as_float(xlo[j]), acc[rt][ct]);
+                        for (int j = 0; j < 4; j++)
+                            acc[rt][ct] = mfma_f32(__uint_as_float(whi[j]), __uint_as_float(xhi[j]), acc[rt][ct]);
+                    } else {
+                        acc[rt][ct] = mfma_bf16(wlo, xlo, acc[rt][ct]);
+                        acc[rt][ct] = mfma_bf16(whi, xhi, acc[rt][ct]);
+                    }
+                }
+            }
+            // pin the products here: without it the MFMAs float to their
+            // last use and every tile's operands stay live at once
+            asm volatile("" : "+v"(acc[rt][0]), "+v"(acc[rt][1]));
+        };
+        // fp8: the block-scale fold of a tile's products is deferred until
+        // the next tile's MFMAs are issued, so the VALU never waits on an
+        // MFMA it just issued (products of two tiles live, 16 registers).
+        auto mfma_pair = [&](const i32x8& xv, f32x4& p0, f32x4& p1) __attribute__((always_inline)) {
+            p0 = mfma_fp8(frag8(bf, 0), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
+            p1 = mfma_fp8(frag8(bf, 1), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
+            asm volatile("" : "+v"(p0), "+v"(p1));
+        };
+        auto fold = [&](int rt, const f32x4& p0, const f32x4& p1, float sx) __attribute__((always_inline)) {
+            const float s0 = sx * sb0;
+            const float s1 = MODE == MODE_UP ? sx * sb1 : s0;
+            for (int i = 0; i < 4; i++) acc[rt][0][i] += p0[i] * s0;
+            for (int i = 0; i < 4; i++) acc[rt][1][i] += p1[i] * s1;
+            asm volatile("" : "+v"(acc[rt][0]), "+v"(acc[rt][1]));
+        };
+        // R token tiles, straight-line code (the main loop is instantiated
+        // per live tile count, so nothing here branches), software-pipelined:
+        // a tile's fragments are read from LDS two tiles ahead of its MFMAs
+        // and (fp8) its products are folded after the next tile's MFMAs are
+        // issued.  Scheduling fences keep operands of at most three tiles
+        // live -- with 128 accumulators and the weight ring live, more would
+        // spill.
+        auto fence = []() __attribute__((always_inline)) {
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        i32x8 xs[3];
+        float ss[3] = {0.f, 0.f, 0.f};
+        f32x4 pp[2][2];
+        load_x(0, xs[0], ss[0]);
+        if (R > 1) load_x(1, xs[1], ss[1]);
+        fence();
+        static_for<R>([&](auto tc) __attribute__((always_inline)) {
+            constexpr int t = decltype(tc)::value;
+            if constexpr (DT == DT_FP8) {
+                mfma_pair(xs[t % 3], pp[t & 1][0], pp[t & 1][1]);
+                tile_issued(t);
+                if constexpr (t >= 1) fold(t - 1, pp[(t - 1) & 1][0], pp[(t - 1) & 1][1], ss[(t - 1) % 3]);
+            } else {
+                mma(t, xs[t % 3], ss[t % 3]);
+                tile_issued(t);
+            }
+            if constexpr (t + 2 < R) load_x(t + 2, xs[(t + 2) % 3], ss[(t + 2) % 3]);
+            fence();
+        });
+        if (DT == DT_FP8) {
+            fold(R - 1, pp[(R - 1) & 1][0], pp[(R - 1) & 1][1], ss[(R - 1) % 3]);
+            fence();
+        }
+    };
+
+    static_assert(2 * kMaxKb <= 512, "one weight-scale load per thread");
+    lds_barrier();  // weight scales in LDS (DOWN's slot / weight loads may still be in flight)
+    // Prefetch distances: activations 2 K-steps ahead (a 3-stage LDS ring;
+    // they come from L2), weights RB-1 K-steps ahead in a ring of RB
+    // register sets -- as deep as the registers left by the live
+    // accumulators allow (RB = 4 for up to 12 token tiles, else 3).  The
+    // loop is unrolled by RB so each weight set keeps a fixed name.
+    //
+    // The prefetch is spread over the step: the vector-memory unit accepts
+    // a wave's loads only as fast as it drains them, so issuing all of a
+    // step's loads at once parks every wave at the issue for most of the
+    // step.  Slot s goes out right after the MFMAs of token tile
+    // (s * tiles) / kSlots, so the activation slots go first.
+    auto step = [&](auto stc, auto rc, auto rbc, bool a_live, int kt, BFrag& cur, BFrag& refill)
+                    __attribute__((always_inline)) {
+        constexpr int R = decltype(rc)::value;  // token tiles per step
+        constexpr int RB = decltype(rbc)::value;
+        // Issue order per step: activation slots of step kt+2, then the 4
+        // weight loads of step kt+RB-1.  Everything of step kt has landed
+        // once at most kWait vector-memory instructions are outstanding:
+        //   RB == 5: the weights of steps kt+1..kt+3 (12) -- for a wave
+        //            with activation slots this also covers the activations
+        //            of step kt, which precede 4 + kASlots + 4 >= 12 later
+        //            instructions;
+        //   RB == 3: the weights of step kt+1 (4), which follow the
+        //            activations of step kt+1 (those are thus waited for
+        //            one step early).
+        //   RB == 4: the weights of steps kt+1, kt+2 (8) -- for a wave with
+        //            activation slots, whose step-kt activations precede
+        //            4 + kASlots + 4 later instructions, this also waits for
+        //            the first activation slot of step kt+1 (one count for
+        //            all waves: no path mixes the two).
+        static_assert(RB == 5 || RB == 4 || RB == 3, "wait counts are derived for rings of 3, 4 or 5 sets");
+        wait_vmcnt<RB == 5 ? 12 : (RB == 4 ? 8 : 4)>();
+        // the weights of this step have landed: pin every use of them below
+        // the wait (the loads were asm, invisible to the compiler's waits)
+        pin(cur);
+        bare_barrier();
+        auto tile_issued = [&](int rt) __attribute__((always_inline)) {
+            for (int sl = 0; sl < kSlots; sl++)
+                if ((sl * R) / kSlots == rt) issue_slot(sl, a_live, kt + 2, kt + RB - 1, refill);
+        };
+        compute(rc, cur, kt, tile_issued);
+    };
+    // The weight registers are written by asm loads the compiler cannot see
+    // as pending, so nothing may copy them before their wait: the prologue
+    // sits inside each instantiation, next to its loop, so the register
+    // sets are defined and consumed in one place with no moves between.
+    auto main_loop = [&](auto rc) __attribute__((always_inline)) {
+        constexpr int R = decltype(rc)::value;
+        constexpr int RB = R <= 12 ? 4 : 3;
+        const std::integral_constant<int, RB> rbc;
+        const bool a_live = 32 * wave < 16 * R;  // uniform
+        // only the live token tiles' accumulators exist during the loop
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        BFrag bs[RB];
+        // prologue, in the steady-state issue order: per step the
+        // activation slots (steps 0, 1) before the weight slots
+        static_for<RB - 1>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            for (int sl = 0; sl < kSlots; sl++)
+                if (sl >= kASlots || i < 2) issue_slot(sl, a_live, i, i, bs[i]);
+        });
+        for (int kt = 0; kt < nk; kt += RB) {
+            static_for<RB>([&](auto stc) __attribute__((always_inline)) {
+                constexpr int ST = decltype(stc)::value;
+                if (ST == 0 || kt + ST < nk) step(stc, rc, rbc, a_live, kt + ST, bs[ST], bs[(ST + RB - 1) % RB]);
+            });
+        }
+        // drain the trailing (out-of-range) prefetches before the ring and
+        // the weight registers are reused
+        wait_vmcnt<0>();
+        static_for<RB>([&](auto ic) __attribute__((always_inline)) { pin(bs[decltype(ic)::value]); });
+#pragma unroll
+        for (int i = R; i < 16; i++)
+            for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    // The loop is instantiated per live token-tile count: fp8 (the layer's
+    // headline path, where an expert's 128 +- 11 rows would otherwise be
+    // rounded up to 192) in steps of one 16-row tile, the fp32 / bf16 paths
+    // in groups of four.
+    const int ntiles = (rows + 15) / 16;  // 1..16, uniform
+    if constexpr (DT == DT_FP8) {
+        static_for<16>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int R = decltype(ic)::value + 1;
+            if (ntiles == R) main_loop(std::integral_constant<int, R>());
+        });
+    } else {
+        switch ((ntiles + 3) / 4) {
+            case 1: main_loop(std::integral_constant<int, 4>()); break;
+            case 2: main_loop(std::integral_constant<int, 8>()); break;
+            case 3: main_loop(std::integral_constant<int, 12>()); break;
+            default: main_loop(std::integral_constant<int, 16>()); break;
+        }
+    }
+    if (MODE == MODE_DOWN && tid < kBM) {
+        ((int*)(smem + kRowInfoOff))[tid] = row_slot;
+        ((float*)(smem + kRowInfoOff))[kBM + tid] = row_w;
+    }
+    __syncthreads();  // every wave is done with the ring before it is reused; row info in LDS
+
+    // ---- epilogues (LDS staging for coalesced 16-byte stores), 128 rows
+    //      per pass; every wave holds all rows of its columns ----
+    float* Tb = (float*)smem;
+    const int er = tid >> 2, pp = tid & 3;  // staged row, 32-column part
+    if (MODE == MODE_UP) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            if (128 * half >= rows) continue;  // uniform; unrolled so acc[] stays in registers
+            if (half) __syncthreads();
+#pragma unroll
+            for (int r8 = 0; r8 < 8; r8++) {
+                const int rt = 8 * half + r8;
+                f32x4 hv;
+                for (int i = 0; i < 4; i++) {
+                    const float gv = acc[rt][0][i], uv = acc[rt][1][i];
+                    // fp32 keeps the reference's expf and IEEE division
+                    // (naive_moe.cu:297-310); the bf16 / fp8 epilogues use
+                    // the hardware exp2 and reciprocal (~1 ulp each)
+                    const float silu = DT == DT_F32 ? gv / (1.0f + expf(-gv))
+                                                    : gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
+                    hv[i] = silu * uv;
+                }
+                *(f32x4*)&Tb[(16 * r8 + r16) * kEpiPitch + 16 * wave + 4 * q] = hv;
+            }
+            __syncthreads();
+            const int rr = 128 * half + er;
+            const int col = nt * 128 + 32 * pp;
+            const bool ok = rr < rows && col < g.n_out;
+            float v[32];
+            for (int j = 0; j < 32; j++) v[j] = ok ? Tb[er * kEpiPitch + 32 * pp + j] : 0.0f;
+            const size_t pos = (size_t)row0 + rr;
+            if (DT == DT_FP8) {
+                float amax = 0.0f;
+                for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+                amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
+                amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+                const float s = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 1.0f;
+                // q = v * (1/s): one correctly rounded reciprocal per block
+                // instead of 32 divisions (codes may differ from v / s by one
+                // step where v / s lies within an ulp of an e4m3 midpoint)
+                const float inv = __fdiv_rn(1.0f, s);
+                if (ok) {
+                    u32x4 o0, o1;
+                    for (int k = 0; k < 4; k++) {
+                        o0[k] = f32x4_to_e4m3x4(v[4 * k] * inv, v[4 * k + 1] * inv,
+                                                v[4 * k + 2] * inv, v[4 * k + 3] * inv);
+                        o1[k] = f32x4_to_e4m3x4(v[16 + 4 * k] * inv, v[16 + 4 * k + 1] * inv,
+                                                v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
+                    }
+                    uint8_t* dst = g.out + pos * g.n_out + col;
+                    *(u32x4*)dst = o0;
+                    *(u32x4*)(dst + 16) = o1;
+                    if (pp == 0) g.out_scale[pos * (g.n_out / 128) + nt] = s;
+                }
+            } else if (DT == DT_BF16) {
+                if (ok) {
+                    uint8_t* dst = g.out + (pos * g.n_out + col) * 2;
+                    for (int k = 0; k < 4; k++) {
+                        u32x4 o;
+                        for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(v[8 * k + 2 * m], v[8 * k + 2 * m + 1]);
+                        *(u32x4*)(dst + 16 * k) = o;
+                    }
+                }
+            } else {
+                if (ok) {
+                    float* dst = (float*)g.out + pos * g.n_out + col;
+                    for (int k = 0; k < 8; k++)
+                        *(f32x4*)(dst + 4 * k) = (f32x4){v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+                }
+            }
+        }
+    } else {
+        // lane (q, r16) holds output columns n0 + 32w + 16ct + 4q .. +3 of
+        // token row 16 rt + r16; the row's slot and routing weight come from
+        // LDS (staged in the prologue)
+        const int* s_slot = (const int*)(smem + kRowInfoOff);
+        const float* s_wt = (const float*)(smem + kRowInfoOff) + kBM;
+        if (DT == DT_F32) {
+            // fp32 (the reference path): 16-byte stores straight from the accumulators
+#pragma unroll
+            for (int rt = 0; rt < 16; rt++) {
+                if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
+                const int r = 16 * rt + r16;
+                if (r >= rows) continue;
+                const size_t sl = (size_t)s_slot[r];
+                const float wgt = s_wt[r];
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const int n = nt * 256 + 32 * wave + 16 * ct + 4 * q;
+                    if (n >= g.n_out) continue;
+                    *(f32x4*)((float*)g.out + sl * g.n_out + n) = acc[rt][ct] * wgt;
+                }
+            }
+        } else {
+            // bf16: the weighted rows are staged through the (now idle) ring,
+            // 128 rows per pass as bf16 with a 544-byte pitch (16 rows of a
+            // 32-byte piece hit each bank at most twice), then every thread
+            // stores 16 contiguous bytes: one instruction writes two full
+            // 512-byte row segments instead of 16 rows x 32 bytes
+            constexpr int kPitch = 544;
+            uint8_t* stg = smem;
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                if (128 * half >= rows) continue;  // uniform
+                if (half) __syncthreads();          // pass 0's reads are done
+#pragma unroll
+                for (int r8 = 0; r8 < 8; r8++) {
+                    const int rt = 8 * half + r8;
+                    const float wgt = s_wt[16 * rt + r16];
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++) {
+                        const f32x4 v = acc[rt][ct] * wgt;
+                        *(u32x2*)(stg + (16 * r8 + r16) * kPitch + (32 * wave + 16 * ct + 4 * q) * 2) =
+                            (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
+                }
+                lds_barrier();
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int c = tid + 512 * j;       // 16-byte chunk of the pass
+                    const int rr = c >> 5, ch = c & 31;  // row in the pass, chunk in the row
+                    const int r = 128 * half + rr;
+                    const int n = nt * 256 + 8 * ch;
+                    if (r < rows && n < g.n_out) {
+                        const u32x4 v = *(const u32x4*)(stg + rr * kPitch + 16 * ch);
+                        *(u32x4*)(g.out + ((size_t)s_slot[r] * g.n_out + n) * 2) = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- launch
+template <int DT, int MODE, bool PK>
+int launch_gemm_variant(const GemmArgs& g, long max_tiles, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)grouped_gemm_kernel<DT, MODE, PK>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds));
+        attr_set = true;
+    }
+    long work = max_tiles * g.n_tiles_n;
+    long grid = 8 * ceil_div(work, 8);
+    if (grid == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(grid < (1L << 31), "grouped gemm: grid too large (%ld)", grid);
+    hipLaunchKernelGGL((grouped_gemm_kernel<DT, MODE, PK>), dim3((unsigned)grid), dim3(512), kGemmLds,
+                       st, g);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+// defined (explicitly instantiated) in the moe_gemm_<type>.hip files
+#define AMDMOE_GEMM_VARIANT(DT, MODE, PK) \
+    extern template int launch_gemm_variant<DT, MODE, PK>(const GemmArgs&, long, hipStream_t);
+AMDMOE_GEMM_VARIANT(DT_F32, MODE_UP, false)
+AMDMOE_GEMM_VARIANT(DT_F32, MODE_DOWN, false)
+AMDMOE_GEMM_VARIANT(DT_BF16, MODE_UP, false)
+AMDMOE_GEMM_VARIANT(DT_BF16, MODE_DOWN, false)
+AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, false)
+AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, true)
+AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, false)
+AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, true)
+#undef AMDMOE_GEMM_VARIANT
+
+}  // namespace amdmoe

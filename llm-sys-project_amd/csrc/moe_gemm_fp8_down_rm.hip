@@ -1,0 +1,8 @@
+// Grouped GEMM kernel variants: <DT_FP8, MODE_DOWN, row-major>.
+#include "moe_gemm.hpp"
+
+namespace amdmoe {
+
+template int launch_gemm_variant<DT_FP8, MODE_DOWN, false>(const GemmArgs&, long, hipStream_t);
+
+}  // namespace amdmoe
