@@ -61,3 +61,44 @@ def violations(asm_text):
                         break
                 j += 1
     return bad
+
+
+def _sregs(tok):
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"s(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def sgpr_hazards(asm_text, states=5):
+    """[(kernel, line, instruction)] for every asm weight load whose scalar
+    operands (descriptor, soffset) were written by a VALU instruction
+    (v_readfirstlane, v_cmp, ...) fewer than `states` wait states before it:
+    the hardware needs 5, and the compiler does not pad before inline asm.
+    Walks back along the fall-through path (s_nop N counts N + 1)."""
+    lines = [ln.split(";")[0].strip() for ln in asm_text.split("\n")]
+    bad, kern = [], None
+    for i, ln in enumerate(lines):
+        m = re.match(r"^(_Z\w+):$", ln)
+        if m:
+            kern = m.group(1)
+        m = re.match(r"buffer_load_dwordx4 v\[\d+:\d+\], v\d+, (s\[\d+:\d+\]), (s\d+) offen", ln)
+        if not m:
+            continue
+        want = _sregs(m.group(1)) | _sregs(m.group(2))
+        ws, j = 0, i - 1
+        while j >= 0 and ws < states:
+            t = lines[j]
+            j -= 1
+            if not t or t.startswith(".") or t.endswith(":") or t.startswith(";"):
+                continue
+            ops = re.split(r"[ ,]+", t)
+            if ops[0] == "s_nop":
+                ws += int(ops[1], 0) + 1
+                continue
+            if ops[0].startswith("v_") and len(ops) > 1 and _sregs(ops[1]) & want:
+                bad.append((kern, i + 1, f"{t}  ->  {ln}"))
+                break
+            ws += 1
+    return bad

@@ -9,7 +9,7 @@ import subprocess
 
 import pytest
 
-from isa_hazards import violations
+from isa_hazards import sgpr_hazards, violations
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SRCS = sorted(glob.glob(os.path.join(ROOT, "llm-sys-project_amd", "csrc", "moe_gemm_*.hip")))
@@ -23,6 +23,17 @@ def test_checker_flags_a_copy_before_the_wait():
     assert len(violations(asm)) == 1
     clean = asm.replace("\tv_mov_b32_e32 v9, v3\n\ts_waitcnt vmcnt(0)", "\ts_waitcnt vmcnt(0)\n\tv_mov_b32_e32 v9, v3")
     assert violations(clean) == []
+
+
+def test_sgpr_checker_flags_a_valu_written_soffset():
+    asm = "\n".join([
+        "_Zk:", "\tv_readfirstlane_b32 s4, v3",
+        "\tbuffer_load_dwordx4 v[2:5], v1, s[0:3], s4 offen offset:0", "\ts_endpgm"])
+    assert len(sgpr_hazards(asm)) == 1
+    padded = asm.replace("s4, v3\n", "s4, v3\n\ts_nop 4\n")
+    assert sgpr_hazards(padded) == []
+    salu = asm.replace("v_readfirstlane_b32 s4, v3", "s_add_i32 s4, s5, 64")
+    assert sgpr_hazards(salu) == []
 
 
 def test_checker_follows_branches_to_a_use():
@@ -50,4 +61,6 @@ def test_grouped_gemm_weight_loads_are_never_touched_in_flight(tmp_path):
         asm = out.read_text()
         assert asm.count("buffer_load_dwordx4 v[") > 0, src
         bad = violations(asm)
+        assert bad == [], (src, bad[:5])
+        bad = sgpr_hazards(asm)
         assert bad == [], (src, bad[:5])
