@@ -98,8 +98,179 @@ def dsa_bench(amdmoe, synth, iters=20):
             "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
 
 
+def _time_calls(fn, iters, warmup=3):
+    """Mean ms of fn() over iters calls, hip events on torch's current stream
+    (the stream every amdmoe wrapper launches on by default)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def sweep(amdmoe, synth, iters):
+    """Every MoE / DSA configuration of BASELINE.json, one row each.
+
+    floor_ms = max(algorithmic HBM bytes / 8 TB/s, FLOPs / dense peak) --
+    the roofline of the whole layer; attainable = floor_ms / ms."""
+    import torch
+    rows = []
+
+    def row(name, dtype, T, E, K, D, I, ms, w_bytes, act_bytes, peak, active):
+        flops = 6 * T * K * D * I
+        nbytes = w_bytes + act_bytes
+        floor = max(nbytes / HBM_PEAK, flops / peak) * 1e3
+        r = {"config": name, "dtype": dtype, "T": T, "E": E, "K": K, "D": D, "I": I,
+             "experts_active": active, "ms": round(ms, 4),
+             "tokens_per_s": round(T / (ms * 1e-3), 1),
+             "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+             "mfma_peak_frac": round(flops / (ms * 1e-3) / peak, 4),
+             "hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+             "floor_ms": round(floor, 4), "attainable_frac": round(floor / ms, 4)}
+        log(f"[sweep] {name:34s} {ms:9.4f} ms  {r['tokens_per_s']:12.1f} tok/s  "
+            f"{r['tflops']:8.2f} TFLOP/s  {100 * r['mfma_peak_frac']:5.1f}% peak  "
+            f"{100 * r['attainable_frac']:5.1f}% of floor {floor:.4f} ms")
+        rows.append(r)
+
+    def active_experts(idx_fn, T, E, K):
+        idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+        wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+        idx_fn(idx, wts)
+        torch.cuda.synchronize()
+        return int(torch.unique(idx).numel())
+
+    # tiny and medium fp32 (reference signature: no gate bias), medium bf16 with bias
+    for name, (T, E, K, D, I) in (("tiny_fp32", (4, 4, 2, 64, 128)),
+                                  ("medium_fp32", (512, 8, 2, 1024, 2048))):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(11)
+        x = torch.randn((T, D), generator=g, device="cuda")
+        wg = torch.randn((E, D), generator=g, device="cuda") / D ** 0.5
+        w1 = torch.randn((E, 2 * I, D), generator=g, device="cuda") / D ** 0.5
+        w2 = torch.randn((E, D, I), generator=g, device="cuda") / I ** 0.5
+        y = torch.empty((T, D), device="cuda")
+        cfg = amdmoe.moe_config(T, E, K, D, I)
+        ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_F32)
+        act = active_experts(lambda i, w: amdmoe.moe_gate_f32(x, wg, i, w, cfg), T, E, K)
+        ms = _time_calls(lambda: amdmoe.moe_forward_f32(x, wg, w1, w2, y, cfg, ws=ws), iters)
+        row(name, "f32", T, E, K, D, I, ms, act * 3 * I * D * 4 + E * D * 4,
+            2 * T * D * 4, 157.3e12, act)
+        del x, wg, w1, w2, y, ws
+    bf16_cfgs = [("medium_bf16_bias", (512, 8, 2, 1024, 2048), True)]
+    bf16_cfgs += [(f"mixtral_bf16_T{T}", (T, 8, 2, 4096, 14336), False) for T in (16, 256, 4096)]
+    layer = None
+    for name, (T, E, K, D, I), bias in bf16_cfgs:
+        if layer is None or layer[0] != (E, D, I, bias) or layer[1].shape[0] < T:
+            layer = None
+            torch.cuda.empty_cache()
+            Tg = 4096 if D == 4096 else T
+            layer = ((E, D, I, bias),) + synth.bf16_layer(Tg, E, D, I, seed=7, bias=bias)
+        xa, wg, b, w1, w2 = layer[1:]
+        x = xa[:T].contiguous()
+        y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+        cfg = amdmoe.moe_config(T, E, K, D, I)
+        ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_BF16)
+        act = active_experts(lambda i, w: amdmoe.moe_gate_bf16x(x, wg, b, i, w, cfg), T, E, K)
+        ms = _time_calls(lambda: amdmoe.moe_forward_bf16(x, wg, b, w1, w2, y, cfg, ws=ws), iters)
+        row(name, "bf16", T, E, K, D, I, ms, act * 3 * I * D * 2 + E * D * 4,
+            2 * T * D * 2, 2.5e15, act)
+        del x, y, ws
+    layer = None
+    torch.cuda.empty_cache()
+    # DeepSeek-V3 fp8 block-scale, packed (headline layout) and row-major
+    E, K, D, I = 256, 8, 7168, 2048
+    w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=1234)
+    w1p, w2p = torch.empty_like(w1q), torch.empty_like(w2q)
+    amdmoe.pack_weights_fp8(w1q, w1p)
+    amdmoe.pack_weights_fp8(w2q, w2p)
+    xa, wg = synth.dsv3_inputs(8192, E, D, seed=99)
+    for T in (1, 64, 512, 4096, 8192):
+        x = xa[:T].contiguous()
+        y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+        cfg = amdmoe.moe_config(T, E, K, D, I)
+        ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_FP8)
+        act = active_experts(lambda i, w: amdmoe.moe_gate_bf16(x, wg, i, w, cfg), T, E, K)
+        wb = act * (3 * I * D + ((2 * I // 128) * (D // 128) + (D // 128) * (I // 128)) * 4) + E * D * 2
+        for lay, (a1, a2, fwd) in (("packed", (w1p, w2p, amdmoe.moe_forward_fp8_packed)),
+                                   ("row-major", (w1q, w2q, amdmoe.moe_forward_fp8))):
+            ms = _time_calls(lambda: fwd(x, wg, a1, w1s, a2, w2s, y, cfg, ws=ws), iters)
+            row(f"dsv3_fp8_T{T}_{lay}", "fp8_e4m3", T, E, K, D, I, ms, wb, 2 * T * D * 2,
+                FP8_PEAK, act)
+        del x, y, ws
+    del w1q, w1s, w2q, w2s, w1p, w2p, xa, wg
+    torch.cuda.empty_cache()
+    return rows
+
+
+def kernel_label(name):
+    """Short label of a demangled kernel name from a rocprofv3 CSV."""
+    import re
+    base = name.split("(")[0].replace("void ", "").replace("amdmoe::", "").strip()
+    m = re.match(r"grouped_gemm_kernel<(\d), (\d), (true|false)>", base)
+    if m:
+        dt = ("f32", "bf16", "fp8")[int(m.group(1))]
+        mode = ("UP", "DOWN")[int(m.group(2))]
+        lay = "packed" if m.group(3) == "true" else "row-major"
+        return f"grouped_gemm_kernel<{dt}, {mode}, {lay}>"
+    return base
+
+
+def pmc_summary(csv_dir, out_md, title, command):
+    """Per-kernel averages of a rocprofv3 --pmc run (counter_collection CSV):
+    each counter summed over its dimension rows per dispatch, then averaged
+    over the kernel's dispatches.  Writes a markdown table to out_md."""
+    import csv
+    import glob
+    from collections import defaultdict
+    files = glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {csv_dir}")
+    per = defaultdict(lambda: defaultdict(float))   # (kernel, dispatch) -> counter -> value
+    dur = {}
+    for fn in files:
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                key = (kernel_label(r["Kernel_Name"]), r["Dispatch_Id"])
+                per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+                if r.get("End_Timestamp"):
+                    dur[key] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+    agg = defaultdict(lambda: defaultdict(list))
+    counters = []
+    for (k, _d), cv in per.items():
+        for c, v in cv.items():
+            agg[k][c].append(v)
+            if c not in counters:
+                counters.append(c)
+    lines = [f"# {title}", "", "Command (from the repository root on the GPU box):", "", "```",
+             command, "```", "",
+             "Per kernel: each counter summed over its hardware instances per dispatch, averaged "
+             "over the kernel's dispatches.", "",
+             "| kernel | dispatches | " + " | ".join(counters) + " |",
+             "|---|---:|" + "---:|" * len(counters)]
+    for k in sorted(agg, key=lambda k: -max(sum(v) for v in agg[k].values())):
+        n = max(len(v) for v in agg[k].values())
+        vals = [sum(agg[k][c]) / len(agg[k][c]) if agg[k][c] else float("nan") for c in counters]
+        lines.append(f"| `{k}` | {n} | " + " | ".join(f"{v:.4g}" for v in vals) + " |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
+        # bench.py --pmc-summary CSV_DIR OUT_MD TITLE COMMAND
+        pmc_summary(*sys.argv[2:6])
+        return
     ap = argparse.ArgumentParser()
+    ap.add_argument("--sweep", metavar="JSON",
+                    help="instead of the headline line, time every BASELINE MoE config and "
+                         "write the rows to JSON")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -123,6 +294,13 @@ def main():
     import amdmoe
     import synth
     torch.cuda.set_device(0)
+    if args.sweep:
+        rows = sweep(amdmoe, synth, args.steps)
+        rows.append({"config": "dsa_decode_B64_H128_S2048", **dsa_bench(amdmoe, synth)})
+        log(f"[sweep] dsa: {rows[-1]}")
+        with open(args.sweep, "w") as f:
+            json.dump(rows, f, indent=1)
+        return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)

@@ -133,8 +133,9 @@ int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const flo
                           void* stream);
 
 /* Routing for the fp8 layer: bf16 x, bf16 gate, logits on bf16 MFMA.  When
- * E <= 256 and D % 64 == 0 the logits pass through the library's cached
- * per-device scratch (T*E*4 bytes, allocated on first use); calls sharing it
+ * E <= 256 and D % 64 == 0 the gate GEMM is split along D and its partial
+ * logits pass through the library's cached per-device scratch (at most
+ * T*E*4*16 bytes, allocated on first use); calls sharing it
  * must be ordered on one stream. */
 int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
                          float* expert_weights, const MoeConfig* cfg, void* stream);

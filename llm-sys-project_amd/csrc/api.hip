@@ -2,7 +2,7 @@
 // layout, and the forward orchestration.  A forward is a fixed sequence of
 // launches on the caller's stream with no host synchronisation and no
 // allocation when a workspace is supplied:
-//   route (R1) -> [fp8: quantise x 1x128] -> permute (R2)
+//   route (R1; fp8: the gate GEMM also quantises x 1x128) -> permute (R2)
 //   -> grouped GEMM up + SwiGLU (R3/R4) -> grouped GEMM down + weight (R5)
 //   -> combine (ascending-expert sum per token)
 // The reference's moe_forward (kernels/moe/naive_moe.cu:400-471) instead
@@ -84,7 +84,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
         w.act = take(P * I);
         w.act_s = (float*)take(4 * P * (I / 128));
         w.ypair = take(2 * P * D);
-        w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E));
+        w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E, (int)D, true));
     } else {
         const size_t es = elem_size(dtype);
         w.act = take(es * P * I);
@@ -295,15 +295,18 @@ static int forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uin
     MoeWs w;
     TRY(resolve_ws(c, AMDMOE_DTYPE_FP8, workspace, workspace_bytes, &w));
     TRY(mark(0, st));
-    if (route_mfma_supported(c.num_experts, c.hidden_dim))
+    if (route_mfma_supported(c.num_experts, c.top_k, c.hidden_dim)) {
+        // the gate GEMM also quantises x (it reads every x element once)
         TRY(launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
-                              w.idx, w.wts, w.logits, st));
-    else
+                              w.idx, w.wts, w.logits, w.xq, w.xs, st));
+        TRY(mark(1, st));
+    } else {
         TRY(launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, c.num_tokens,
                                                    c.num_experts, c.top_k, c.hidden_dim, w.idx,
                                                    w.wts, st));
-    TRY(mark(1, st));
-    TRY(launch_quant_rows(x, c.num_tokens, c.hidden_dim, w.xq, w.xs, st));
+        TRY(mark(1, st));
+        TRY(launch_quant_rows(x, c.num_tokens, c.hidden_dim, w.xq, w.xs, st));
+    }
     TRY(mark(2, st));
     return moe_experts(DT_FP8, c, w, w.xq, w.xs, w1, w1_scale, w2, w2_scale, y, st, packed);
 }
@@ -355,13 +358,15 @@ int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* ex
                          float* expert_weights, const MoeConfig* cfg, void* stream) {
     TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
     if (cfg->num_tokens == 0) return AMDMOE_OK;
-    if (route_mfma_supported(cfg->num_experts, cfg->hidden_dim)) {
+    if (route_mfma_supported(cfg->num_experts, cfg->top_k, cfg->hidden_dim)) {
         // logits scratch: the library's cached per-device workspace
         void* scratch = nullptr;
-        TRY(cached_workspace(route_mfma_scratch_bytes(cfg->num_tokens, cfg->num_experts), &scratch));
+        TRY(cached_workspace(route_mfma_scratch_bytes(cfg->num_tokens, cfg->num_experts,
+                                                      cfg->hidden_dim, false),
+                             &scratch));
         return launch_route_mfma(x, gate_weight, cfg->num_tokens, cfg->num_experts, cfg->top_k,
                                  cfg->hidden_dim, expert_indices, expert_weights, (float*)scratch,
-                                 (hipStream_t)stream);
+                                 nullptr, nullptr, (hipStream_t)stream);
     }
     return launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, cfg->num_tokens,
                                                   cfg->num_experts, cfg->top_k, cfg->hidden_dim,

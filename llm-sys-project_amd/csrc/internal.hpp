@@ -39,11 +39,13 @@ struct GemmArgs {
 template <typename XT, typename GT>
 int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int E, int K, int D,
                        int* idx, float* wts, hipStream_t st);
-bool route_mfma_supported(int E, int D);
-// logits: scratch of route_mfma_scratch_bytes(T, E)
-size_t route_mfma_scratch_bytes(int T, int E);
+bool route_mfma_supported(int E, int K, int D);
+// part: scratch of route_mfma_scratch_bytes(T, E, D, quant) bytes (split-K
+// partial logits).  quant: xq [T,D] e4m3 and xs [T,D/128] are also written
+// (the 1x128 activation quantisation of x, D % 128 == 0); else both null.
+size_t route_mfma_scratch_bytes(int T, int E, int D, bool quant);
 int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
-                      float* wts, float* logits, hipStream_t st);
+                      float* wts, float* part, uint8_t* xq, float* xs, hipStream_t st);
 
 // moe_permute.hip
 // scratch: permute_scratch_bytes(T, E) bytes, or nullptr (single-launch

@@ -47,8 +47,21 @@ __device__ __forceinline__ float row_min16(float v, int width) {
     return v;
 }
 
-// Routing of one token by one wave, E <= 256: `v` holds the logits of
-// experts lane + 64j (j < 4; -FLT_MAX past E).
+// min over the slot lanes [0, KMAX) of a 16-lane DPP row, broadcast from
+// lane 0 (lanes in [K, KMAX) must hold +inf).
+template <int KMAX>
+__device__ __forceinline__ float slot_min(float v) {
+    static_assert(KMAX >= 1 && KMAX <= 16, "slot_min: KMAX <= 16");
+    if constexpr (KMAX > 1) v = dpp_min<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (KMAX > 2) v = dpp_min<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (KMAX > 4) v = dpp_min<0x141>(v);  // row_half_mirror
+    if constexpr (KMAX > 8) v = dpp_min<0x140>(v);  // row_mirror
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+// Routing of one token by one wave, E <= 256, K <= KMAX <= 16: `v` holds
+// the logits of experts lane + 64j (j < 4; -FLT_MAX past E).
+template <int KMAX>
 __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, float* out_wts) {
     const int lane = lane_id();
     // softmax (tests/test_moe.cu:14-20)
@@ -59,59 +72,44 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
     // The denominator is summed in ascending expert order, exactly as the
     // reference does: lane values are read out one by one (v_readlane).
     float s = 0.0f;
-    const int nj = (E + 63) / 64;
-    for (int j = 0; j < nj; j++) {
-        const float x = pick4(v, j);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (64 * j >= E) break;  // uniform
         const int n = min(64, E - 64 * j);
         if (n == 64) {
 #pragma unroll
             for (int l = 0; l < 64; l++)
-                s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+                s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l)));
         } else {
-            for (int l = 0; l < n; l++) s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)));
+            for (int l = 0; l < n; l++) s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l)));
         }
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) v[j] = __fdiv_rn(v[j], s);
 
-    // replace-min top-K.  Lane k < K owns slot k.  The victim is the first
-    // slot holding the smallest value: its value comes from a DPP min over
-    // the slot lanes (K <= 16) and its position from a ballot of the lanes
-    // equal to it.
+    // replace-min top-K (tests/test_moe.cu:52-64).  Lane k < K owns slot k.
+    // thr is the smallest slot value and m the first slot holding it; only
+    // an expert with p > thr changes anything, and thr never decreases, so
+    // the experts of each 64-lane group that beat the current thr are taken
+    // in ascending order from a ballot mask, which is re-formed after every
+    // insertion from the new thr.
     float sv = -FLT_MAX;
     int si = -1;
-    auto argmin_slot = [&](float& thr) -> int {
-        const float mine = lane < K ? sv : INFINITY;
-        float mv;
-        if (K <= 16) {
-            mv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(row_min16(mine, K))));
-        } else {
-            mv = mine;
-            for (int o = 1; o < kWave; o <<= 1) mv = fminf(mv, __shfl_xor(mv, o, kWave));
-            mv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(mv)));
-        }
-        thr = mv;
-        return __ffsll(__ballot(lane < K && sv == mv)) - 1;
-    };
-    float thr;
-    int m = argmin_slot(thr);
-    int pos = 0;
-    while (pos < E) {
-        // first expert e >= pos with p_e > thr: experts are lane-major per
-        // register, so the first register with a hit holds the smallest e
-        int found = E;
+    float thr = -FLT_MAX;  // every slot starts at -FLT_MAX: the first victim is slot 0
+    int m = 0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = lane + 64 * j;
-            const unsigned long long b = __ballot(e < E && e >= pos && v[j] > thr);
-            if (found == E && b) found = 64 * j + __ffsll(b) - 1;
+    for (int j = 0; j < 4; j++) {
+        if (64 * j >= E) break;  // uniform
+        const bool valid = lane + 64 * j < E;
+        unsigned long long cand = __ballot(valid && v[j] > thr);
+        while (cand) {
+            const int l = __ffsll(cand) - 1;  // next inserted expert: 64j + l
+            const float val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+            if (lane == m) { sv = val; si = 64 * j + l; }
+            thr = slot_min<KMAX>(lane < K ? sv : INFINITY);
+            m = __ffsll(__ballot(lane < K && sv == thr)) - 1;
+            cand = __ballot(valid && lane > l && v[j] > thr);
         }
-        if (found >= E) break;
-        const float val = __int_as_float(
-            __builtin_amdgcn_readlane(__float_as_int(pick4(v, found >> 6)), found & 63));
-        if (lane == m) { sv = val; si = found; }
-        pos = found + 1;
-        m = argmin_slot(thr);
     }
     // renormalise in slot order (tests/test_moe.cu:65-68)
     float tot = 0.0f;
@@ -122,6 +120,10 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
         out_wts[lane] = tot > 0.0f ? __fdiv_rn(sv, tot) : sv;
     }
 }
+
+// Smallest power of two >= K (K <= 16): the slot-lane width of
+// wave_route_token_reg.
+static inline int route_kmax(int K) { return K <= 1 ? 1 : K <= 2 ? 2 : K <= 4 ? 4 : K <= 8 ? 8 : 16; }
 
 // Generic form for any E: probabilities in LDS (overwrites `p`).
 __device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float* out_wts) {
@@ -174,12 +176,15 @@ __device__ void wave_route_token_lds(float* p, int E, int K, int* out_idx, float
 }
 
 __device__ __forceinline__ void wave_route_token(float* p, int E, int K, int* out_idx, float* out_wts) {
-    if (E <= 256) {
+    if (E <= 256 && K <= 16) {
         const int lane = lane_id();
         float v[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? p[lane + 64 * j] : -FLT_MAX;
-        wave_route_token_reg(v, E, K, out_idx, out_wts);
+        if (K <= 2) wave_route_token_reg<2>(v, E, K, out_idx, out_wts);
+        else if (K <= 4) wave_route_token_reg<4>(v, E, K, out_idx, out_wts);
+        else if (K <= 8) wave_route_token_reg<8>(v, E, K, out_idx, out_wts);
+        else wave_route_token_reg<16>(v, E, K, out_idx, out_wts);
     } else {
         wave_route_token_lds(p, E, K, out_idx, out_wts);
     }
@@ -229,53 +234,95 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
 // ---------------------------------------------------------------- MFMA
 // bf16 x [T,D] and bf16 Wg [E,D], E <= 256, D % 64 == 0.  Two launches:
 //
-// route_logits_kernel: the gate GEMM, logits [T,E] fp32 into a scratch
-//   buffer.  Block = 256 threads, a 32-token x 128-expert tile (wave w owns
-//   experts [32w, 32w+32): 2 row tiles x 2 column tiles of 16x16 MFMA).
-//   Each K-step (64 bf16 = 128 bytes of every row) streams the x rows (4 KB)
-//   and the gate rows (16 KB) global -> LDS through a 3-stage direct-load
-//   ring, so two steps are in flight while one is consumed; rows past T or E
-//   read as zeros.  LDS rows are 128 bytes, 16-byte chunks XOR-swizzled by
-//   (row & 7).  With T/32 x E/128 blocks (256 at T=4096, E=256) every CU
-//   streams; the gate matrix is re-read per token tile from L2.
-// route_topk_kernel: one wave per token (softmax + replace-min top-K +
-//   renormalisation, wave_route_token_reg), 4 tokens per block, so a CU
-//   interleaves many tokens' latency-bound shuffle chains.
-constexpr int kRtTok = 32;
-constexpr int kRtExp = 128;
-constexpr int kRtStage = (kRtTok + kRtExp) * 128;  // 20480
+// route_logits_kernel: the gate GEMM, split along D.  Block = 512 threads,
+//   a 64-token x 256-expert tile over one K-chunk (wave w owns experts
+//   [32w, 32w+32): 4 row tiles x 2 column tiles of 16x16 MFMA).  Each K-step
+//   (64 bf16 = 128 bytes of every row) streams the x rows (8 KB) and the
+//   gate rows (32 KB) global -> LDS through a 3-stage direct-load ring; rows
+//   past T or E read as zeros.  LDS rows are 128 bytes, 16-byte chunks
+//   XOR-swizzled by (row & 7).  The grid is (token tiles) x (K-chunks),
+//   with as many chunks as it takes to give every CU a block (4 at
+//   T=4096; at most 16, 14 at T=1), so no block walks all of D alone; every x element is
+//   read by exactly one block.  Each chunk's partial logits go to
+//   part[chunk][T][E] (fp32).
+//   Fused x quantisation (fp8 layer): a chunk covers whole 128-column
+//   blocks (two K-steps), so the block that reads a token's columns also
+//   writes their e4m3 codes and 1x128 scale -- the even K-step's 64 values
+//   are held in registers until the odd one arrives.  Same arithmetic as
+//   quant_rows_kernel (scale = amax/448, q = e4m3_rne_sat(v/scale)), so the
+//   codes are bit-identical.
+// route_topk_kernel: one wave per token: sums the chunk partials in chunk
+//   order, then softmax + replace-min top-K + renormalisation
+//   (wave_route_token_reg).
+constexpr int kRtTok = 64;
+constexpr int kRtExp = 256;
+constexpr int kRtStage = (kRtTok + kRtExp) * 128;  // 40960
 constexpr int kRtNS = 3;
-constexpr int kRtLds = kRtNS * kRtStage;           // 61440
+constexpr int kRtLds = kRtNS * kRtStage;           // 122880
+constexpr int kRtMinBlocks = 256;                  // one per CU
+constexpr int kRtMaxSplit = 16;                    // partials summed per logit
 
-__global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __restrict__ x,
+// K-steps (64 columns) per chunk and number of chunks.  With quantisation
+// a chunk is a whole number of 128-column blocks.
+struct RouteSplit {
+    int kc, nsplit;
+};
+static RouteSplit route_split(int T, int D, bool quant) {
+    const int nk = D / 64, unit = quant ? 2 : 1;
+    const int units = nk / unit;
+    const int tiles = (T + kRtTok - 1) / kRtTok;
+    int want = (kRtMinBlocks + tiles - 1) / tiles;
+    want = want > kRtMaxSplit ? kRtMaxSplit : want;
+    want = want < 1 ? 1 : (want > units ? units : want);
+    const int kc = ((units + want - 1) / want) * unit;
+    return {kc, (nk + kc - 1) / kc};
+}
+
+// max over the 8 lanes of a DPP half-row
+template <int CTRL>
+__device__ __forceinline__ float dpp_fmax(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                                CTRL, 0xF, 0xF, false)));
+}
+
+__global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ wg, int T,
-                                                           int E, int D, float* __restrict__ logits) {
+                                                           int E, int D, int kc,
+                                                           float* __restrict__ part,
+                                                           uint8_t* __restrict__ xq,
+                                                           float* __restrict__ xs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t0 = blockIdx.x * kRtTok, e0 = blockIdx.y * kRtExp;
+    const int t0 = blockIdx.x * kRtTok, split = blockIdx.y;
     const int nk = D / 64;
+    const int kb0 = split * kc;
+    const int nloc = min(nk, kb0 + kc) - kb0;  // >= 1 (even with quantisation)
     const long row_bytes = (long)D * 2;
 
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (long)T * row_bytes);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wg, (long)E * row_bytes);
     const int lrow = lane >> 3, lchunk = (lane & 7) ^ lrow;
-    // x: 4 slabs of 8 rows (one per wave); Wg: 16 slabs (4 per wave)
+    // x: 8 slabs of 8 rows (one per wave); Wg: 32 slabs (4 per wave)
     const int xr = t0 + 8 * wave + lrow;
     const uint32_t voff_x = xr < T ? (uint32_t)(xr * row_bytes + 16 * lchunk) : kOob;
     uint32_t voff_w[4];
     for (int j = 0; j < 4; j++) {
-        const int r = e0 + 32 * wave + 8 * j + lrow;
+        const int r = 32 * wave + 8 * j + lrow;
         voff_w[j] = r < E ? (uint32_t)(r * row_bytes + 16 * lchunk) : kOob;
     }
-    // rotated K order per block: gate rows are 128-byte slices at a fixed
-    // stride, so blocks in lockstep would all hit the same memory channels
-    const int kt0 = (int)(((unsigned)blockIdx.x * 13u) % (unsigned)nk);
+    // rotated K order per block (by whole 128-column blocks): gate rows are
+    // 128-byte slices at a fixed stride, so blocks in lockstep would all hit
+    // the same memory channels
+    const int npair = nloc >> 1;
+    const int kt0 = npair > 1 ? 2 * (int)(((unsigned)blockIdx.x * 13u) % (unsigned)npair) : 0;
+    auto kloc = [&](int kt) {
+        int k = kt + kt0;
+        return k >= nloc ? k - nloc : k;
+    };
     auto issue = [&](int st, int kt) {
         uint8_t* base = smem + st * kRtStage;
-        kt += kt0;
-        if (kt >= nk) kt -= nk;
-        const int soff = kt * 128;
+        const int soff = (kb0 + kloc(kt)) * 128;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16, voff_x, soff, 0, 0);
         for (int j = 0; j < 4; j++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -284,20 +331,26 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
 
     const int q = lane >> 4, r16 = lane & 15;
     const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
-    f32x4 acc[2][2];
-    for (int i = 0; i < 2; i++)
+    f32x4 acc[4][2];
+    for (int i = 0; i < 4; i++)
         for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+    // quantisation: thread (token tq, chunk qc) owns 8 columns of each half
+    const int tq = tid >> 3, qc = tid & 7;
+    const int qtok = t0 + tq;
+    float qv[8];
+    float qam = 0.0f;
+
     issue(0, 0);
-    if (nk > 1) issue(1, 1);
-    for (int kt = 0; kt < nk; kt++) {
-        if (kt + 1 < nk) wait_vmcnt<5>();
+    if (nloc > 1) issue(1, 1);
+    for (int kt = 0; kt < nloc; kt++) {
+        if (kt + 1 < nloc) wait_vmcnt<5>();
         else wait_vmcnt<0>();
         bare_barrier();
-        if (kt + 2 < nk) issue((kt + 2) % kRtNS, kt + 2);
+        if (kt + 2 < nloc) issue((kt + 2) % kRtNS, kt + 2);
         const uint8_t* base = smem + (kt % kRtNS) * kRtStage;
-        u32x4 alo[2], ahi[2];
-        for (int rt = 0; rt < 2; rt++) {
+        u32x4 alo[4], ahi[4];
+        for (int rt = 0; rt < 4; rt++) {
             const uint8_t* p = base + (16 * rt + r16) * 128;
             alo[rt] = *(const u32x4*)(p + off_lo);
             ahi[rt] = *(const u32x4*)(p + off_hi);
@@ -305,34 +358,85 @@ __global__ __launch_bounds__(256) void route_logits_kernel(const uint16_t* __res
         for (int ct = 0; ct < 2; ct++) {
             const uint8_t* p = base + (kRtTok + 32 * wave + 16 * ct + r16) * 128;
             const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
-            for (int rt = 0; rt < 2; rt++) {
+            for (int rt = 0; rt < 4; rt++) {
                 acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
                 acc[rt][ct] = mfma_bf16(ahi[rt], bhi, acc[rt][ct]);
             }
         }
+        if (xq) {
+            const u32x4 raw = *(const u32x4*)(base + tq * 128 + 16 * (qc ^ (tq & 7)));
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                f[2 * k] = __uint_as_float(raw[k] << 16);
+                f[2 * k + 1] = __uint_as_float(raw[k] & 0xffff0000u);
+            }
+            float am = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(f[k]));
+            am = dpp_fmax<0x141>(dpp_fmax<0x4E>(dpp_fmax<0xB1>(am)));  // 8-lane max
+            const int kg = kb0 + kloc(kt);                              // global K-step
+            if ((kg & 1) == 0) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) qv[k] = f[k];
+                qam = am;
+            } else if (qtok < T) {
+                am = fmaxf(am, qam);
+                const float sc = am > 0.0f ? __fdiv_rn(am, 448.0f) : 1.0f;
+                const int blk = kg >> 1;
+                uint8_t* dst = xq + (size_t)qtok * D + blk * 128 + 8 * qc;
+                u32x2 c0, c1;
+                c0[0] = f32x4_to_e4m3x4(__fdiv_rn(qv[0], sc), __fdiv_rn(qv[1], sc), __fdiv_rn(qv[2], sc), __fdiv_rn(qv[3], sc));
+                c0[1] = f32x4_to_e4m3x4(__fdiv_rn(qv[4], sc), __fdiv_rn(qv[5], sc), __fdiv_rn(qv[6], sc), __fdiv_rn(qv[7], sc));
+                c1[0] = f32x4_to_e4m3x4(__fdiv_rn(f[0], sc), __fdiv_rn(f[1], sc), __fdiv_rn(f[2], sc), __fdiv_rn(f[3], sc));
+                c1[1] = f32x4_to_e4m3x4(__fdiv_rn(f[4], sc), __fdiv_rn(f[5], sc), __fdiv_rn(f[6], sc), __fdiv_rn(f[7], sc));
+                *(u32x2*)dst = c0;
+                *(u32x2*)(dst + 64) = c1;
+                if (qc == 0) xs[(size_t)qtok * (D / 128) + blk] = sc;
+            }
+        }
     }
-    // lane (q, r16) holds logits of tokens 16rt + 4q + i, expert 16ct + r16
-    for (int rt = 0; rt < 2; rt++)
+    // lane (q, r16) holds logits of tokens 16rt + 4q + i, expert 32w + 16ct + r16
+    float* dst = part + (size_t)split * T * E;
+    for (int rt = 0; rt < 4; rt++)
         for (int ct = 0; ct < 2; ct++) {
-            const int e = e0 + 32 * wave + 16 * ct + r16;
+            const int e = 32 * wave + 16 * ct + r16;
             for (int i = 0; i < 4; i++) {
                 const int t = t0 + 16 * rt + 4 * q + i;
-                if (e < E && t < T) logits[(size_t)t * E + e] = acc[rt][ct][i];
+                if (e < E && t < T) dst[(size_t)t * E + e] = acc[rt][ct][i];
             }
         }
 }
 
-__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int T,
-                                                         int E, int K, int* __restrict__ idx,
+template <int KMAX>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ part, int nsplit,
+                                                         int T, int E, int K, int* __restrict__ idx,
                                                          float* __restrict__ wts) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;  // whole wave
-    const float* row = logits + (size_t)t * E;
     float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? row[lane + 64 * j] : -FLT_MAX;
-    wave_route_token_reg(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
+    for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? 0.0f : -FLT_MAX;
+    // the partials of 8 chunks are loaded before any is added, then summed
+    // in chunk order
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+        float pv[8][4];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float* row = part + ((size_t)(s0 + i) * T + t) * E;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                pv[i][j] = s0 + i < nsplit && lane + 64 * j < E ? row[lane + 64 * j] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (s0 + i < nsplit)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (lane + 64 * j < E) v[j] = add_rn(v[j], pv[i][j]);
+    }
+    wave_route_token_reg<KMAX>(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
 // ---------------------------------------------------------------- launch
@@ -358,18 +462,38 @@ template int launch_route_exact<uint16_t, uint16_t>(const uint16_t*, const uint1
                                                     const float*, int, int, int, int, int*,
                                                     float*, hipStream_t);
 
-bool route_mfma_supported(int E, int D) { return E >= 1 && E <= 256 && D % 64 == 0; }
+bool route_mfma_supported(int E, int K, int D) { return E >= 1 && E <= 256 && K <= 16 && D % 64 == 0; }
 
-size_t route_mfma_scratch_bytes(int T, int E) { return (size_t)T * E * sizeof(float); }
+size_t route_mfma_scratch_bytes(int T, int E, int D, bool quant) {
+    return (size_t)route_split(T, D, quant).nsplit * T * E * sizeof(float);
+}
 
 int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K, int D, int* idx,
-                      float* wts, float* logits, hipStream_t st) {
-    AMDMOE_CHECK_ARG(route_mfma_supported(E, D), "routing: MFMA gate needs E <= 256 and D %% 64 == 0");
-    dim3 g1((unsigned)ceil_div(T, kRtTok), (unsigned)ceil_div(E, kRtExp));
-    hipLaunchKernelGGL(route_logits_kernel, g1, dim3(256), kRtLds, st, x, wg, T, E, D, logits);
+                      float* wts, float* part, uint8_t* xq, float* xs, hipStream_t st) {
+    AMDMOE_CHECK_ARG(route_mfma_supported(E, K, D), "routing: MFMA gate needs E <= 256, K <= 16 and D %% 64 == 0");
+    const bool quant = xq != nullptr;
+    AMDMOE_CHECK_ARG(!quant || (xs && D % 128 == 0), "routing: fused quantisation needs D %% 128 == 0");
+    const RouteSplit sp = route_split(T, D, quant);
+    static bool attr_set = false;
+    if (!attr_set) {
+        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)route_logits_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kRtLds));
+        attr_set = true;
+    }
+    dim3 g1((unsigned)ceil_div(T, kRtTok), (unsigned)sp.nsplit);
+    hipLaunchKernelGGL(route_logits_kernel, g1, dim3(512), kRtLds, st, x, wg, T, E, D, sp.kc, part,
+                       xq, xs);
     AMDMOE_LAUNCH_CHECK();
-    hipLaunchKernelGGL(route_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, logits,
-                       T, E, K, idx, wts);
+    auto topk = route_topk_kernel<16>;
+    switch (route_kmax(K)) {
+        case 1: topk = route_topk_kernel<1>; break;
+        case 2: topk = route_topk_kernel<2>; break;
+        case 4: topk = route_topk_kernel<4>; break;
+        case 8: topk = route_topk_kernel<8>; break;
+        default: break;
+    }
+    hipLaunchKernelGGL(topk, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, part, sp.nsplit, T, E,
+                       K, idx, wts);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
