@@ -247,6 +247,10 @@ def pmc_summary(csv_dir, out_md, title, command):
             agg[k][c].append(v)
             if c not in counters:
                 counters.append(c)
+        if (k, _d) in dur:
+            agg[k]["duration_us"].append(dur[(k, _d)])
+    if dur:
+        counters.append("duration_us")
     lines = [f"# {title}", "", "Command (from the repository root on the GPU box):", "", "```",
              command, "```", "",
              "Per kernel: each counter summed over its hardware instances per dispatch, averaged "

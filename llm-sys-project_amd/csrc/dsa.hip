@@ -613,8 +613,10 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
 // the wave stores O to its spare rows B, adds B into its partial rows A in
 // memory, scaled to the new max, and restarts O at zero.  This is a rare
 // path: with O(1) scores the first tile's max is never exceeded by 8.
-// Every split writes its unnormalised O (fp32, rows A) and (max, sum) per
-// head; dsa_merge_kernel combines the splits and writes bf16.
+// Every split writes its unnormalised O (bf16: the output is bf16 and the
+// merge sums at most a few splits in fp32) and (max, sum) per head;
+// dsa_merge_kernel combines the splits and writes bf16.  The fp32 rows A and
+// B serve only the rare rescale path.
 //
 // Tile layout (tile32_off): 1 KB blocks of 16 tokens x 4 chunks (16-byte
 // chunk j of the 1152-byte row), blocks [token group][chunk group], within a
@@ -676,7 +678,7 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
     const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
     const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,
-    float* __restrict__ part_ml, int Q, int H,
+    uint16_t* __restrict__ part_b, float* __restrict__ part_ml, int Q, int H,
     int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int* s_rows = (int*)(smem + kRows32Off);
@@ -920,13 +922,30 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     }
     wait_vmcnt<0>();  // the trailing (out-of-range) tile loads
 
-    // the split's partial: A = O (+ A if part of O was flushed), m, l
+    // the split's partial, bf16 in the accumulator order (512 contiguous
+    // bytes per store): O, or, if part of O was flushed, A + O
+    uint16_t* pb_base = part_b + prow0 * kDc + lane_off;
+    asm volatile("" : "+v"(pb_base));
     if (!flushed) {
-        store_o(part_o);
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++)
+#pragma unroll
+            for (int mt = 0; mt < 32; mt++)
+                *(u32x2*)(pb_base + 16 * kDc * ht + 256 * mt) =
+                    (u32x2){pack_bf16x2(o[mt][ht][0], o[mt][ht][1]), pack_bf16x2(o[mt][ht][2], o[mt][ht][3])};
     } else {
         store_o(spare_o);
         const float one[2] = {1.0f, 1.0f};
         fold_b(false, one);
+        const float* a = part_o + prow0 * kDc + lane_off;
+#pragma unroll
+        for (int ht = 0; ht < 2; ht++)
+#pragma unroll 4
+            for (int mt = 0; mt < 32; mt++) {
+                const size_t off = 16 * kDc * ht + 256 * mt;
+                const f32x4 v = *(const f32x4*)(a + off);
+                *(u32x2*)(pb_base + off) = (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            }
     }
 #pragma unroll
     for (int ht = 0; ht < 2; ht++) {
@@ -939,8 +958,8 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
 // the split maxima, weights c_j = 2^(m_j - m), out = (sum c_j O_j) /
 // (sum c_j l_j), bf16.  Workgroup = one query x 16 heads (one partial block),
 // wave w = dim tiles 8w..8w+7 in the block's accumulator order: every load
-// is 1 KB contiguous, and lane (g, c) holds dims 16mt + 4g + i of head c.
-__global__ __launch_bounds__(256) void dsa_merge_kernel(const float* __restrict__ part_o,
+// is 512 bytes contiguous, and lane (g, c) holds dims 16mt + 4g + i of head c.
+__global__ __launch_bounds__(256) void dsa_merge_kernel(const uint16_t* __restrict__ part_b,
                                                         const float* __restrict__ part_ml,
                                                         uint16_t* __restrict__ out, int Q,
                                                         int H, int nsplit) {
@@ -965,9 +984,17 @@ __global__ __launch_bounds__(256) void dsa_merge_kernel(const float* __restrict_
         const float2 ml = *(const float2*)(part_ml + 2 * (blk + c16));
         const float c = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - m);
         L += c * ml.y;
-        const f32x4* po = (const f32x4*)(part_o + blk * kDc) + 64 * 8 * wave + lane;
+        const u32x2* po = (const u32x2*)(part_b + blk * kDc) + 64 * 8 * wave + lane;
+        u32x2 pv[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) acc[k] += c * po[64 * k];
+        for (int k = 0; k < 8; k++) pv[k] = po[64 * k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            acc[k][0] += c * __uint_as_float(pv[k][0] << 16);
+            acc[k][1] += c * __uint_as_float(pv[k][0] & 0xffff0000u);
+            acc[k][2] += c * __uint_as_float(pv[k][1] << 16);
+            acc[k][3] += c * __uint_as_float(pv[k][1] & 0xffff0000u);
+        }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     uint16_t* orow = out + ((size_t)qi * H + h) * kDc + 4 * g;
@@ -991,7 +1018,8 @@ static int dsa_nsplit(int Q, int H, int S) {
 size_t dsa_paged_scratch_bytes(int Q, int H, int S) {
     if (Q <= 0 || H % 128 != 0 || S < 1) return 0;  // the kernels without splits
     const size_t rows = (size_t)Q * dsa_nsplit(Q, H, S) * H;
-    return 2 * rows * kDc * 4 + align_up(rows * 8, 256);  // rows A, spare rows B, (m, l)
+    // rows A, spare rows B (fp32), the bf16 partials, (m, l)
+    return 2 * rows * kDc * 4 + rows * kDc * 2 + align_up(rows * 8, 256);
 }
 
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
@@ -1023,13 +1051,14 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
         const size_t rows_bytes = (size_t)Q * ns * H * kDc * 4;
         float* part_o = (float*)scratch;
         float* spare_o = (float*)((uint8_t*)scratch + rows_bytes);
-        float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes);
+        uint16_t* part_b = (uint16_t*)((uint8_t*)scratch + 2 * rows_bytes);
+        float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes + rows_bytes / 2);
         hipLaunchKernelGGL(dsa_split_kernel, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
                            qp, cache, cache_tokens * kRowBytes, page_table, logical, part_o, spare_o,
-                           part_ml, Q, H, S, page, pages_per_seq, ns, chunk, scale_log2);
+                           part_b, part_ml, Q, H, S, page, pages_per_seq, ns, chunk, scale_log2);
         AMDMOE_LAUNCH_CHECK();
         hipLaunchKernelGGL(dsa_merge_kernel, dim3((unsigned)(ceil_div((long)Q * (H / 16), 8) * 8)),
-                           dim3(256), 0, st, (const float*)part_o, (const float*)part_ml, out, Q, H, ns);
+                           dim3(256), 0, st, (const uint16_t*)part_b, (const float*)part_ml, out, Q, H, ns);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
     }
