@@ -140,6 +140,16 @@ int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const flo
 int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
                          float* expert_weights, const MoeConfig* cfg, void* stream);
 
+/* Routing for the fp8 layer together with the 1x128 quantisation of x, as
+ * the fp8 forward runs it: the gate GEMM reads every x element once and
+ * also writes xq e4m3 [T,D] and x_scale fp32 [T,D/128] (the format of
+ * amdmoe_quant_rows_fp8; D % 128 == 0).  expert_indices / expert_weights as
+ * amdmoe_moe_gate_bf16, whose scratch rules apply.  No counterpart in the
+ * reference (fp32 only); its routing is moe_gate (naive_moe.cuh:27-29). */
+int amdmoe_moe_gate_fp8(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
+                        float* expert_weights, uint8_t* xq, float* x_scale, const MoeConfig* cfg,
+                        void* stream);
+
 /* Per-expert gather: replaces moe_gather (naive_moe.cuh:38-41,
  * naive_moe.cu:357-366).  Tokens routed to expert_id in ascending token
  * order: gathered [cnt,D], token_map [cnt], *count (device int). */

@@ -19,7 +19,7 @@ SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
     "amdmoe_moe_forward_f32", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
     "amdmoe_moe_forward_fp8_packed", "amdmoe_pack_weights_fp8",
-    "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16",
+    "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16", "amdmoe_moe_gate_fp8",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
     "amdmoe_quant_weight_fp8", "amdmoe_set_stage_events", "amdmoe_dsa_forward_f32",
@@ -75,6 +75,7 @@ def load():
         "amdmoe_moe_gate_f32": (I, [_P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16x": (I, [_P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16": (I, [_P, _P, _P, _P, cfgp, _P]),
+        "amdmoe_moe_gate_fp8": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gather_f32": (I, [_P, _P, _P, I, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_permute": (I, [_P, cfgp, _P, _P, _P, _P, _P]),
         "amdmoe_naive_gemm_f32": (I, [_P, _P, _P, I, I, I, _P]),
@@ -189,6 +190,11 @@ def moe_gate_bf16x(x, wg, bias, idx, wts, cfg, stream=None):
 def moe_gate_bf16(x, wg, idx, wts, cfg, stream=None):
     _check(load().amdmoe_moe_gate_bf16(_ptr(x), _ptr(wg), _ptr(idx), _ptr(wts),
                                        ctypes.byref(cfg), _stream(stream)))
+
+
+def moe_gate_fp8(x, wg, idx, wts, xq, xs, cfg, stream=None):
+    _check(load().amdmoe_moe_gate_fp8(_ptr(x), _ptr(wg), _ptr(idx), _ptr(wts), _ptr(xq), _ptr(xs),
+                                      ctypes.byref(cfg), _stream(stream)))
 
 
 def moe_gather_f32(x, idx, wts, expert, gathered, token_map, count, cfg, stream=None):

@@ -374,6 +374,28 @@ int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* ex
                                                   (hipStream_t)stream);
 }
 
+int amdmoe_moe_gate_fp8(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
+                        float* expert_weights, uint8_t* xq, float* x_scale, const MoeConfig* cfg,
+                        void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_FP8));
+    AMDMOE_CHECK_ARG(x && gate_weight && expert_indices && expert_weights && xq && x_scale,
+                     "null tensor pointer");
+    const MoeConfig& c = *cfg;
+    if (c.num_tokens == 0) return AMDMOE_OK;
+    hipStream_t st = (hipStream_t)stream;
+    if (route_mfma_supported(c.num_experts, c.top_k, c.hidden_dim)) {
+        void* scratch = nullptr;
+        TRY(cached_workspace(route_mfma_scratch_bytes(c.num_tokens, c.num_experts, c.hidden_dim, true),
+                             &scratch));
+        return launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
+                                 expert_indices, expert_weights, (float*)scratch, xq, x_scale, st);
+    }
+    TRY(launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, c.num_tokens, c.num_experts,
+                                               c.top_k, c.hidden_dim, expert_indices,
+                                               expert_weights, st));
+    return launch_quant_rows(x, c.num_tokens, c.hidden_dim, xq, x_scale, st);
+}
+
 int amdmoe_moe_gather_f32(const float* x, const int* expert_indices, const float* expert_weights,
                           int expert_id, float* gathered, int* token_map, int* count,
                           const MoeConfig* cfg, void* stream) {

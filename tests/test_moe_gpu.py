@@ -110,6 +110,43 @@ def test_gate_bf16_mfma_bit_exact_on_exact_logits(amd, orc, T, E, K, D):
     np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6, atol=0)
 
 
+@pytest.mark.parametrize("T,E,K,D", [(1, 256, 8, 7168), (70, 256, 8, 7168), (4096, 256, 8, 7168),
+                                     (33, 64, 6, 512)])
+def test_gate_fp8_fused_quant_bit_exact(amd, orc, T, E, K, D):
+    """Routing of the fp8 layer with the x quantisation fused into the gate
+    GEMM (the forward's path): codes and scales bit-identical to the oracle's
+    1x128 quantiser, expert indices bit-exact on exactly representable logits."""
+    announce(f"gate_fp8 fused quant T={T} E={E} K={K} D={D}")
+    cfg = amd.moe_config(T, E, K, D, 128)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    q = torch.empty((T, D), dtype=torch.uint8, device="cuda")
+    s = torch.empty((T, D // 128), dtype=torch.float32, device="cuda")
+    # 1) exactly representable logits: indices and weights as the oracle's
+    x, wg = _exact_gate_inputs(T, E, D, 13)
+    xb, wgb = orc.f32_to_bf16(x), orc.f32_to_bf16(wg)
+    idx_ref, wts_ref = orc.moe_route(x, wg, K)
+    amd.moe_gate_fp8(dev(xb), dev(wgb), idx, wts, q, s, cfg)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6, atol=0)
+    np.testing.assert_array_equal(host(q), orc.quant_rows_1x128(x)[0])
+    # 2) random x over a wide range, an all-zero block and subnormal codes:
+    #    e4m3 codes and scales bit-identical to the oracle's quantiser
+    rng = np.random.default_rng(T + D)
+    x = rng.standard_normal((T, D)).astype(np.float32) * np.float32(4.0)
+    x *= np.exp2(rng.integers(-6, 7, (T, 1))).astype(np.float32)
+    x[0, :128] = 0.0
+    x[-1, -128:] *= np.float32(2.0 ** -12)
+    x[-1, -128] = np.float32(1.0)
+    xb = orc.f32_to_bf16(x)
+    q_ref, s_ref = orc.quant_rows_1x128(orc.bf16_to_f32(xb))
+    amd.moe_gate_fp8(dev(xb), dev(wgb), idx, wts, q, s, cfg)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(s), s_ref)
+    np.testing.assert_array_equal(host(q), q_ref)
+
+
 def test_gate_bf16_mfma_random_margin_aware(amd, orc):
     """Random N(0,1) inputs at the DSV3 gate shape.  GPU (MFMA) and CPU
     (sequential) logits differ by rounding, so the selected set must match
@@ -238,6 +275,22 @@ def test_forward_f32_reference_cases(amd, orc, name, shape, tol):
     assert err < 1e-5 * max(1.0, np.abs(y_ref).max())
 
 
+@pytest.mark.parametrize("T,E,K,D,I", [(1024, 4, 2, 128, 256), (512, 4, 2, 64, 128),
+                                       (600, 3, 2, 64, 128)])
+def test_forward_f32_multi_mtile_experts(amd, orc, T, E, K, D, I):
+    """Experts of 2-3 M-tiles and of 1-2 M-tiles (a full 256-row tile plus
+    a small one), on the reference's inputs, at the fp32 bar."""
+    announce(f"forward_f32 multi-M-tile experts {(T, E, K, D, I)}")
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    _, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
+    y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), y, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    err = np.abs(host(y) - y_ref).max()
+    print(f"multi-M-tile f32: max_err={err:.3e}")
+    assert err < 1e-5 * max(1.0, np.abs(y_ref).max())
+
+
 def test_forward_f32_explicit_workspace_and_reuse(amd, orc):
     T, E, K, D, I = 64, 16, 2, 512, 1024
     x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
@@ -286,6 +339,15 @@ def test_forward_bf16_mixtral_t16(amd, orc):
     announce("forward_bf16 mixtral T=16")
     err, _ = _bf16_case(amd, orc, 16, 8, 2, 4096, 14336, bias=False)
     assert err < 1e-2
+
+
+def test_forward_bf16_multi_mtile_experts(amd, orc):
+    """~512 rows per expert: each expert spans 2-3 M-tiles of 256 rows.  The
+    outputs reach |y| ~ 3, where one bf16 step is 1.6e-2, so the bar is
+    relative: 2^-7 of max |y|."""
+    announce("forward_bf16 multi-M-tile experts")
+    err, y_ref = _bf16_case(amd, orc, 1024, 4, 2, 128, 256, bias=True)
+    assert err < 2.0 ** -7 * np.abs(y_ref).max()
 
 
 def test_forward_bf16_mixtral_t4096_sampled(amd, orc):
@@ -338,6 +400,15 @@ def test_forward_fp8_small_full(amd, orc):
     announce("forward_fp8 small full")
     w = synth.dsv3_weights(16, 512, 256, seed=77)
     assert _fp8_case(amd, orc, w, 64, 16, 4, 512, 256) < 2e-2
+
+
+def test_forward_fp8_multi_mtile_experts(amd, orc):
+    """~256 rows per expert (as DeepSeek-V3 at T=8192): experts take one or
+    two M-tiles."""
+    import synth
+    announce("forward_fp8 multi-M-tile experts")
+    w = synth.dsv3_weights(4, 256, 128, seed=81)
+    assert _fp8_case(amd, orc, w, 512, 4, 2, 256, 128) < 2e-2
 
 
 def test_forward_fp8_dsv3_t1(amd, orc, dsv3):
