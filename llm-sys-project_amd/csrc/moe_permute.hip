@@ -267,6 +267,122 @@ __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int* __res
     }
 }
 
+// Scan and scatter in one launch (nblk <= kFusedMaxBlk): every 64-token
+// block derives its own offsets.  Thread j handles experts j, j + 256, ...:
+// pre = sum of its counts over the blocks before this one, tot = over all
+// blocks; a block-wide exclusive scan of tot (and of the M-tile counts) over
+// experts gives the expert's first row (and first M-tile); the block's rows
+// for expert e start at row_off[e] + pre[e].  Block 0 also writes counts,
+// offsets and the M-tile table.  Reading all of blk_cnt per block costs
+// nblk * E * 4 bytes of L2 reads per block (64 KB at T=4096, E=256).
+constexpr int kFusedMaxBlk = 128;
+constexpr int kFusedThreads = 256;
+constexpr int kFusedMaxE = 1024;
+
+__global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
+    const int* __restrict__ idx, int T, int K, int E, int BM, const int* __restrict__ blk_cnt,
+    int nblk, int* __restrict__ counts, int* __restrict__ offsets, int4* __restrict__ tiles,
+    int* __restrict__ num_tiles, int* __restrict__ sorted_token, int* __restrict__ sorted_slot,
+    const float* __restrict__ wts, float* __restrict__ sorted_w) {
+    __shared__ int s_off[kFusedMaxE];                  // this block's first row per expert
+    __shared__ unsigned long long s_mask[kFusedMaxE];  // token lane masks per expert
+    __shared__ int s_wr[kFusedThreads / 64], s_wt[kFusedThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x;
+    constexpr int kEpt = kFusedMaxE / kFusedThreads;  // experts per thread (at most)
+    int pre[kEpt], tot[kEpt];
+#pragma unroll
+    for (int i = 0; i < kEpt; i++) {
+        const int e = tid + kFusedThreads * i;
+        pre[i] = 0;
+        tot[i] = 0;
+        if (e < E) {
+            // loads of 8 blocks in flight before they are summed
+            for (int b0 = 0; b0 < nblk; b0 += 8) {
+                int v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = b0 + j < nblk ? blk_cnt[(size_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    tot[i] += v[j];
+                    if (b0 + j < b) pre[i] += v[j];
+                }
+            }
+        }
+    }
+    // exclusive scan over experts in the order e = tid + 256 i: a thread's
+    // experts are not contiguous, so scan per i-slice: experts of slice i
+    // follow all experts of slices < i
+    int row_base = 0, tile_base = 0;
+#pragma unroll
+    for (int i = 0; i < kEpt; i++) {
+        if (kFusedThreads * i >= E) break;  // uniform
+        const int r = tot[i], tl = (tot[i] + BM - 1) / BM;
+        // inclusive wave scan
+        int rs = r, ts = tl;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ro = __shfl_up(rs, o, 64), to = __shfl_up(ts, o, 64);
+            if (lane >= o) { rs += ro; ts += to; }
+        }
+        if (lane == 63) { s_wr[wave] = rs; s_wt[wave] = ts; }
+        __syncthreads();
+        int wr = 0, wt = 0, ar = 0, at = 0;
+        for (int w = 0; w < kFusedThreads / 64; w++) {
+            if (w < wave) { wr += s_wr[w]; wt += s_wt[w]; }
+            ar += s_wr[w];
+            at += s_wt[w];
+        }
+        __syncthreads();
+        const int e = tid + kFusedThreads * i;
+        const int row_off = row_base + wr + rs - r, tile_off = tile_base + wt + ts - tl;
+        if (e < E) {
+            s_off[e] = row_off + pre[i];
+            if (b == 0) {
+                counts[e] = tot[i];
+                offsets[e] = row_off;
+                for (int j = 0; j < tl; j++)
+                    tiles[tile_off + j] = make_int4(e, row_off + j * BM, min(BM, tot[i] - j * BM), 0);
+            }
+        }
+        row_base += ar;
+        tile_base += at;
+    }
+    if (b == 0 && tid == 0) {
+        offsets[E] = row_base;
+        *num_tiles = tile_base;
+    }
+    // this block's 64 tokens: lane masks per expert, then every first
+    // occurrence goes to its row
+    for (int e = tid; e < E; e += kFusedThreads) s_mask[e] = 0ull;
+    __syncthreads();
+    const int t = b * kPermTok + lane;
+    const int* row = idx + (size_t)t * K;
+    if (wave == 0 && t < T) {
+        for (int k = 0; k < K; k++) {
+            const int v = row[k];
+            if (v < 0 || v >= E) continue;
+            bool dup = false;
+            for (int j = 0; j < k; j++) dup |= row[j] == v;
+            if (!dup) atomicOr(&s_mask[v], 1ull << lane);
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && t < T) {
+        const unsigned long long below = (1ull << lane) - 1ull;
+        for (int k = 0; k < K; k++) {
+            const int v = row[k];
+            if (v < 0 || v >= E) continue;
+            bool dup = false;
+            for (int j = 0; j < k; j++) dup |= row[j] == v;
+            if (dup) continue;
+            const int pos = s_off[v] + __popcll(s_mask[v] & below);
+            sorted_token[pos] = t;
+            sorted_slot[pos] = t * K + k;
+            if (sorted_w) sorted_w[pos] = wts[(size_t)t * K + k];
+        }
+    }
+}
+
 size_t permute_scratch_bytes(int T, int E) {
     const long nblk = (T + kPermTok - 1) / kPermTok;
     if (E > 1024 || nblk * E > (1L << 22)) return 0;
@@ -284,6 +400,13 @@ int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int
         const size_t lds = sizeof(unsigned long long) * (size_t)E;
         hipLaunchKernelGGL(perm_count_kernel, dim3(nblk), dim3(kPermTok), lds, st, idx, T, K, E, blk_cnt);
         AMDMOE_LAUNCH_CHECK();
+        if (nblk <= kFusedMaxBlk && E <= kFusedMaxE) {
+            hipLaunchKernelGGL(perm_scan_scatter_kernel, dim3(nblk), dim3(kFusedThreads), 0, st, idx, T,
+                               K, E, BM, blk_cnt, nblk, counts, offsets, tiles, num_tiles,
+                               sorted_token, sorted_slot, wts, sorted_w);
+            AMDMOE_LAUNCH_CHECK();
+            return AMDMOE_OK;
+        }
         hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(1024), 0, st, blk_cnt, blk_off, nblk, E, BM,
                            counts, offsets, tiles, num_tiles);
         AMDMOE_LAUNCH_CHECK();
