@@ -221,6 +221,102 @@ def kernel_label(name):
     return base
 
 
+def pmc_averages(csv_dir):
+    """{kernel label: {counter: mean per dispatch}} of a rocprofv3 --pmc run
+    (each counter summed over its hardware-instance rows per dispatch, then
+    averaged over the kernel's dispatches), with "dispatches" and, when the
+    CSV has timestamps, "duration_us"."""
+    import csv
+    import glob
+    from collections import defaultdict
+    files = glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {csv_dir}")
+    per = defaultdict(lambda: defaultdict(float))
+    dur = {}
+    for fn in files:
+        with open(fn) as f:
+            for r in csv.DictReader(f):
+                key = (kernel_label(r["Kernel_Name"]), r["Dispatch_Id"])
+                per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+                if r.get("End_Timestamp"):
+                    dur[key] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+    agg = defaultdict(lambda: defaultdict(list))
+    for key, cv in per.items():
+        for c, v in cv.items():
+            agg[key[0]][c].append(v)
+        if key in dur:
+            agg[key[0]]["duration_us"].append(dur[key])
+    return {k: dict({c: sum(v) / len(v) for c, v in cs.items()},
+                    dispatches=max(len(v) for v in cs.values())) for k, cs in agg.items()}
+
+
+def traffic_summary(fetch_dir, write_dir, out_md, out_json, command):
+    """HBM bytes per launch from a FETCH_SIZE run and a WRITE_SIZE run of the
+    same command with --calibrate-copy: the 1 GiB device-to-device copy
+    (rocclr copyBuffer dispatches, 1 GiB read + 1 GiB written in all) gives
+    the factor from each counter's KiB to true bytes."""
+    fa, wa = pmc_averages(fetch_dir), pmc_averages(write_dir)
+    cal = [k for k in fa if "copyBuffer" in k]
+    if not cal:
+        raise SystemExit("no copy-kernel dispatches: run with --calibrate-copy")
+    c = cal[0]
+    per_dispatch_kib = (1 << 30) / 1024 / fa[c]["dispatches"]
+    f_fetch = per_dispatch_kib / fa[c]["FETCH_SIZE"]
+    f_write = per_dispatch_kib / wa[c]["WRITE_SIZE"]
+    rows, kernels = [], {}
+    for k in sorted(fa, key=lambda k: -fa[k]["FETCH_SIZE"]):
+        if k.startswith("at::") or k.startswith("rocprim") or k not in wa or k == c:
+            continue
+        fb = fa[k]["FETCH_SIZE"] * 1024 * f_fetch
+        wb = wa[k]["WRITE_SIZE"] * 1024 * f_write
+        kernels[k] = {"fetch_kib": fa[k]["FETCH_SIZE"], "write_kib": wa[k]["WRITE_SIZE"],
+                      "bytes": fb + wb}
+        rows.append(f"| `{k}` | {fa[k]['FETCH_SIZE']:.4g} | {wa[k]['WRITE_SIZE']:.4g} | "
+                    f"{(fb + wb) / 1e9:.3f} GB |")
+    lines = ["# HBM traffic per launch: DSV3 fp8 MoE layer, T=4096 (+ DSA decode)", "",
+             "Two counter runs and the summary (from the repository root on the GPU box):", "",
+             "```", command, "```", "",
+             f"Calibration: `--calibrate-copy` runs one 1 GiB device-to-device copy first "
+             f"(`{c}`, {fa[c]['dispatches']} dispatches).  Per dispatch FETCH_SIZE reads "
+             f"{fa[c]['FETCH_SIZE']:.0f} KiB and WRITE_SIZE {wa[c]['WRITE_SIZE']:.0f} KiB of "
+             f"{per_dispatch_kib:.0f} KiB moved each way, so bytes = FETCH_SIZE x 1024 x "
+             f"{f_fetch:.2f} + WRITE_SIZE x 1024 x {f_write:.2f}.", "",
+             "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / launch (calibrated) |",
+             "|---|---:|---:|---:|"] + rows
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    with open(out_json, "w") as f:
+        json.dump({"factor_fetch": f_fetch, "factor_write": f_write, "kernels": kernels}, f, indent=1)
+    print("\n".join(lines))
+
+
+def stats_summary(csv_dir, out_md, title, command):
+    """This library's kernels from a rocprofv3 --kernel-trace --stats run
+    (kernel_stats.csv) as a markdown table."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(csv_dir, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_stats.csv under {csv_dir}")
+    lines = [f"# {title}", "", "Command (from the repository root on the GPU box):", "", "```",
+             command, "```", "",
+             "Rows: this library's kernels (torch and rocprim kernels of the synthetic-data "
+             "setup omitted).", "",
+             "| kernel | calls | average us | min us | max us | total share |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for r in csv.DictReader(open(files[0])):
+        k = kernel_label(r["Name"])
+        if k.startswith("at::") or k.startswith("rocprim") or "elementwise" in k:
+            continue
+        lines.append(f"| `{k}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                     f"{float(r['Percentage']):.1f}% |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def pmc_summary(csv_dir, out_md, title, command):
     """Per-kernel averages of a rocprofv3 --pmc run (counter_collection CSV):
     each counter summed over its dimension rows per dispatch, then averaged
@@ -270,6 +366,14 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
         # bench.py --pmc-summary CSV_DIR OUT_MD TITLE COMMAND
         pmc_summary(*sys.argv[2:6])
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--stats-summary":
+        # bench.py --stats-summary CSV_DIR OUT_MD TITLE COMMAND
+        stats_summary(*sys.argv[2:6])
+        return
+    if len(sys.argv) > 1 and sys.argv[1] == "--traffic-summary":
+        # bench.py --traffic-summary FETCH_DIR WRITE_DIR OUT_MD OUT_JSON COMMAND
+        traffic_summary(*sys.argv[2:7])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--sweep", metavar="JSON",

@@ -268,15 +268,17 @@ __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int* __res
 }
 
 // Scan and scatter in one launch (nblk <= kFusedMaxBlk): every 64-token
-// block derives its own offsets.  Thread j handles experts j, j + 256, ...:
-// pre = sum of its counts over the blocks before this one, tot = over all
-// blocks; a block-wide exclusive scan of tot (and of the M-tile counts) over
-// experts gives the expert's first row (and first M-tile); the block's rows
-// for expert e start at row_off[e] + pre[e].  Block 0 also writes counts,
-// offsets and the M-tile table.  Reading all of blk_cnt per block costs
-// nblk * E * 4 bytes of L2 reads per block (64 KB at T=4096, E=256).
+// block derives its own offsets.  Thread (p, e) of NP = 1024 / Ep parts
+// (Ep = E rounded up to a power of two) sums expert e's counts over its
+// range of blocks, all loads in flight together: in total (tot) and over
+// the blocks before this one (pre).  A block-wide exclusive scan of tot
+// (and of the M-tile counts) over experts gives the expert's first row
+// (and first M-tile); the block's rows for expert e start at
+// row_off[e] + pre[e].  Block 0 also writes counts, offsets and the M-tile
+// table.  Every block reads all of blk_cnt: nblk * E * 4 bytes of L2 reads
+// (64 KB at T=4096, E=256).
 constexpr int kFusedMaxBlk = 128;
-constexpr int kFusedThreads = 256;
+constexpr int kFusedThreads = 1024;
 constexpr int kFusedMaxE = 1024;
 
 __global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
@@ -284,72 +286,75 @@ __global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
     int nblk, int* __restrict__ counts, int* __restrict__ offsets, int4* __restrict__ tiles,
     int* __restrict__ num_tiles, int* __restrict__ sorted_token, int* __restrict__ sorted_slot,
     const float* __restrict__ wts, float* __restrict__ sorted_w) {
+    __shared__ int s_full[kFusedThreads], s_pre[kFusedThreads];
     __shared__ int s_off[kFusedMaxE];                  // this block's first row per expert
     __shared__ unsigned long long s_mask[kFusedMaxE];  // token lane masks per expert
     __shared__ int s_wr[kFusedThreads / 64], s_wt[kFusedThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = blockIdx.x;
-    constexpr int kEpt = kFusedMaxE / kFusedThreads;  // experts per thread (at most)
-    int pre[kEpt], tot[kEpt];
-#pragma unroll
-    for (int i = 0; i < kEpt; i++) {
-        const int e = tid + kFusedThreads * i;
-        pre[i] = 0;
-        tot[i] = 0;
+    int Ep = 1;
+    while (Ep < E) Ep <<= 1;
+    const int NP = kFusedThreads / Ep;
+    {
+        const int e = tid % Ep, p = tid / Ep;
+        const int chunk = (nblk + NP - 1) / NP;
+        const int b0 = p * chunk;
+        constexpr int kMaxChunk = kFusedMaxBlk;  // NP >= 1 parts cover nblk <= 128 blocks
+        int full = 0, pre = 0;
         if (e < E) {
-            // loads of 8 blocks in flight before they are summed
-            for (int b0 = 0; b0 < nblk; b0 += 8) {
-                int v[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = b0 + j < nblk ? blk_cnt[(size_t)(b0 + j) * E + e] : 0;
+            int v[8];
+            for (int c0 = 0; c0 < chunk && c0 < kMaxChunk; c0 += 8) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    tot[i] += v[j];
-                    if (b0 + j < b) pre[i] += v[j];
+                    const int bb = b0 + c0 + j;
+                    v[j] = c0 + j < chunk && bb < nblk ? blk_cnt[(size_t)bb * E + e] : 0;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    full += v[j];
+                    if (b0 + c0 + j < b) pre += v[j];
                 }
             }
         }
+        s_full[tid] = full;
+        s_pre[tid] = pre;
     }
-    // exclusive scan over experts in the order e = tid + 256 i: a thread's
-    // experts are not contiguous, so scan per i-slice: experts of slice i
-    // follow all experts of slices < i
-    int row_base = 0, tile_base = 0;
-#pragma unroll
-    for (int i = 0; i < kEpt; i++) {
-        if (kFusedThreads * i >= E) break;  // uniform
-        const int r = tot[i], tl = (tot[i] + BM - 1) / BM;
-        // inclusive wave scan
-        int rs = r, ts = tl;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int ro = __shfl_up(rs, o, 64), to = __shfl_up(ts, o, 64);
-            if (lane >= o) { rs += ro; ts += to; }
+    __syncthreads();
+    // thread e < E: expert totals, then an exclusive scan over experts
+    int tot = 0, pre = 0, tl = 0;
+    if (tid < E) {
+        for (int p = 0; p < NP; p++) {
+            tot += s_full[p * Ep + tid];
+            pre += s_pre[p * Ep + tid];
         }
-        if (lane == 63) { s_wr[wave] = rs; s_wt[wave] = ts; }
-        __syncthreads();
-        int wr = 0, wt = 0, ar = 0, at = 0;
-        for (int w = 0; w < kFusedThreads / 64; w++) {
-            if (w < wave) { wr += s_wr[w]; wt += s_wt[w]; }
-            ar += s_wr[w];
-            at += s_wt[w];
+        tl = (tot + BM - 1) / BM;
+    }
+    int rs = tot, ts = tl;  // inclusive wave scans
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ro = __shfl_up(rs, o, 64), to = __shfl_up(ts, o, 64);
+        if (lane >= o) { rs += ro; ts += to; }
+    }
+    if (lane == 63) { s_wr[wave] = rs; s_wt[wave] = ts; }
+    __syncthreads();
+    int wr = 0, wt = 0, ar = 0, at = 0;
+    for (int w = 0; w < kFusedThreads / 64; w++) {
+        if (w < wave) { wr += s_wr[w]; wt += s_wt[w]; }
+        ar += s_wr[w];
+        at += s_wt[w];
+    }
+    if (tid < E) {
+        const int row_off = wr + rs - tot, tile_off = wt + ts - tl;
+        s_off[tid] = row_off + pre;
+        if (b == 0) {
+            counts[tid] = tot;
+            offsets[tid] = row_off;
+            for (int j = 0; j < tl; j++)
+                tiles[tile_off + j] = make_int4(tid, row_off + j * BM, min(BM, tot - j * BM), 0);
         }
-        __syncthreads();
-        const int e = tid + kFusedThreads * i;
-        const int row_off = row_base + wr + rs - r, tile_off = tile_base + wt + ts - tl;
-        if (e < E) {
-            s_off[e] = row_off + pre[i];
-            if (b == 0) {
-                counts[e] = tot[i];
-                offsets[e] = row_off;
-                for (int j = 0; j < tl; j++)
-                    tiles[tile_off + j] = make_int4(e, row_off + j * BM, min(BM, tot[i] - j * BM), 0);
-            }
-        }
-        row_base += ar;
-        tile_base += at;
     }
     if (b == 0 && tid == 0) {
-        offsets[E] = row_base;
-        *num_tiles = tile_base;
+        offsets[E] = ar;
+        *num_tiles = at;
     }
     // this block's 64 tokens: lane masks per expert, then every first
     // occurrence goes to its row

@@ -243,7 +243,8 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
 //   XOR-swizzled by (row & 7).  The grid is (token tiles) x (K-chunks),
 //   with as many chunks as it takes to give every CU a block (4 at
 //   T=4096; at most 16, 14 at T=1), so no block walks all of D alone; every x element is
-//   read by exactly one block.  Each chunk's partial logits go to
+//   read by exactly one block.  Blocks of one chunk share an XCD (its L2
+//   holds the chunk's gate rows).  Each chunk's partial logits go to
 //   part[chunk][T][E] (fp32).
 //   Fused x quantisation (fp8 layer): a chunk covers whole 128-column
 //   blocks (two K-steps), so the block that reads a token's columns also
@@ -287,14 +288,23 @@ __device__ __forceinline__ float dpp_fmax(float v) {
 
 __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ wg, int T,
-                                                           int E, int D, int kc,
+                                                           int E, int D, int kc, int nsplit,
                                                            float* __restrict__ part,
                                                            uint8_t* __restrict__ xq,
                                                            float* __restrict__ xs) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t0 = blockIdx.x * kRtTok, split = blockIdx.y;
+    // work item (chunk-major, token tile fastest), dealt to the 8 XCDs in
+    // contiguous ranges (workgroup b runs on XCD b % 8): the blocks of one
+    // K-chunk share an XCD, whose L2 then holds that chunk's gate rows
+    // instead of every chunk's
+    const int ntile = (T + kRtTok - 1) / kRtTok;
+    const int per = gridDim.x >> 3;
+    const int item = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (item >= ntile * nsplit) return;  // grid padding
+    const int split = item / ntile;
+    const int t0 = (item - split * ntile) * kRtTok;
     const int nk = D / 64;
     const int kb0 = split * kc;
     const int nloc = min(nk, kb0 + kc) - kb0;  // >= 1 (even with quantisation)
@@ -315,7 +325,7 @@ __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __res
     // 128-byte slices at a fixed stride, so blocks in lockstep would all hit
     // the same memory channels
     const int npair = nloc >> 1;
-    const int kt0 = npair > 1 ? 2 * (int)(((unsigned)blockIdx.x * 13u) % (unsigned)npair) : 0;
+    const int kt0 = npair > 1 ? 2 * (int)(((unsigned)(t0 / kRtTok) * 13u) % (unsigned)npair) : 0;
     auto kloc = [&](int kt) {
         int k = kt + kt0;
         return k >= nloc ? k - nloc : k;
@@ -480,9 +490,10 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kRtLds));
         attr_set = true;
     }
-    dim3 g1((unsigned)ceil_div(T, kRtTok), (unsigned)sp.nsplit);
-    hipLaunchKernelGGL(route_logits_kernel, g1, dim3(512), kRtLds, st, x, wg, T, E, D, sp.kc, part,
-                       xq, xs);
+    // one linear grid, padded to a multiple of 8 for the XCD dealing
+    const long items = ceil_div(T, kRtTok) * (long)sp.nsplit;
+    hipLaunchKernelGGL(route_logits_kernel, dim3((unsigned)(ceil_div(items, 8) * 8)), dim3(512), kRtLds,
+                       st, x, wg, T, E, D, sp.kc, sp.nsplit, part, xq, xs);
     AMDMOE_LAUNCH_CHECK();
     auto topk = route_topk_kernel<16>;
     switch (route_kmax(K)) {
