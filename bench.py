@@ -408,6 +408,18 @@ def main():
         log(f"[sweep] dsa: {rows[-1]}")
         with open(args.sweep, "w") as f:
             json.dump(rows, f, indent=1)
+        md = ["| config | ms | tokens/s | TFLOP/s | % dense peak | floor ms | % of floor |",
+              "|---|---:|---:|---:|---:|---:|---:|"]
+        for r in rows[:-1]:
+            md.append(f"| {r['config']} | {r['ms']:.4f} | {r['tokens_per_s']:.0f} | {r['tflops']:.1f} | "
+                      f"{100 * r['mfma_peak_frac']:.1f}% | {r['floor_ms']:.4f} | "
+                      f"{100 * r['attainable_frac']:.1f}% |")
+        d = rows[-1]
+        md.append(f"| {d['config']} (bf16, paged) | {d['us_per_call'] / 1e3:.4f} | "
+                  f"{d['queries_per_s']:.0f} queries/s | {100 * d['bf16_mfma_frac']:.1f}% of bf16 | | "
+                  f"{0.0212:.4f} | {100 * d['hbm_frac']:.1f}% of HBM peak |")
+        with open(os.path.splitext(args.sweep)[0] + ".md", "w") as f:
+            f.write("\n".join(md) + "\n")
         return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")

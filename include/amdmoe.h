@@ -198,7 +198,9 @@ int amdmoe_quant_weight_fp8(const float* w, long rows, int cols, const float* u,
  * calls with events on stream 0, utils/cuda_utils.cuh:27-50).  While
  * `events` is non-NULL, each MoE forward records events[0..6] (hipEvent_t,
  * owned by the caller) on its stream: [0] start, [1] after routing,
- * [2] after x quantisation (fp8 only; otherwise recorded with [1]),
+ * [2] after x quantisation (fp8 with E > 256 or K > 16, where it is a launch
+ * of its own; otherwise -- including the fp8 layer, whose gate GEMM quantises x
+ * -- recorded right after [1]),
  * [3] after the permutation, [4] after the up-projection GEMM, [5] after
  * the down-projection GEMM, [6] after the combine.  Per host thread;
  * NULL turns it off. */
