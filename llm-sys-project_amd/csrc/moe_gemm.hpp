@@ -235,11 +235,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
     if (sb_pos >= 0) ((float*)(smem + kBScaleOff))[sb_pos] = sb_val;
 
-    // K-steps run in a rotated order starting at kt0, keyed by the M-tile:
+    // K-steps run in a rotated order starting at kt0, keyed by the expert:
     // the N-tiles of one M-tile run together on one XCD and read the same
-    // activation K-slice at the same time (one fetch, the rest L2 hits),
-    // while different M-tiles start at different K offsets.
-    const int kt0 = (int)(((unsigned)mt * 7u) % (unsigned)nk);
+    // activation K-slice at the same time (one fetch, the rest L2 hits), an
+    // expert's M-tiles (evenly sized, adjacent in the item order) read the
+    // same weight K-slices together, and different experts start at
+    // different K offsets.
+    const int kt0 = (int)(((unsigned)e * 7u) % (unsigned)nk);
     auto kblk = [&](int kt) __attribute__((always_inline)) {
         int k = kt + kt0;
         k = k >= nk ? k - nk : k;

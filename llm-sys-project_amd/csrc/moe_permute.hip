@@ -23,6 +23,19 @@ namespace amdmoe {
 
 constexpr int kPermThreads = 1024;
 
+// M-tile j of an expert with `cnt` rows starting at row_off: the expert's
+// ceil(cnt / BM) tiles split its 16-row token tiles as evenly as possible
+// (270 rows -> 144 + 126, not 256 + 14), so the tiles of one expert run
+// at the same pace and stream its weights side by side.
+__device__ __forceinline__ int4 mtile(int e, int row_off, int cnt, int BM, int j) {
+    const int nt = (cnt + BM - 1) / BM;
+    const int q = (cnt + 15) / 16;  // token tiles
+    const int base = q / nt, extra = q % nt;
+    const int first = 16 * (j * base + min(j, extra));
+    const int rows = min(16 * (base + (j < extra ? 1 : 0)), cnt - first);
+    return make_int4(e, row_off + first, rows, 0);
+}
+
 // Slot i = t*K + k counts for expert e = idx[i] only if no earlier slot of
 // the same token holds e (the reference's `break`).  Slots with e outside
 // [0,E) (the -1 left when K > E) count nowhere.
@@ -126,7 +139,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
 
     for (int j = tid; j * BM < cnt; j += kPermThreads) {
         int r0 = j * BM;
-        tiles[tile_off + j] = make_int4(e, row_off + r0, min(BM, cnt - r0), 0);
+        tiles[tile_off + j] = mtile(e, row_off, cnt, BM, j);
     }
     if (tid == 0) {
         counts[e] = cnt;
@@ -231,7 +244,7 @@ __global__ __launch_bounds__(1024) void perm_scan_kernel(const int* __restrict__
             counts[e] = tot;
             offsets[e] = row_off;
             for (int j = 0; j < nt; j++)
-                tiles[tile_off + j] = make_int4(e, row_off + j * BM, min(BM, tot - j * BM), 0);
+                tiles[tile_off + j] = mtile(e, row_off, tot, BM, j);
             if (e == E - 1) {
                 offsets[E] = s_rows[e];
                 *num_tiles = s_tiles[e];
@@ -349,7 +362,7 @@ __global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
             counts[tid] = tot;
             offsets[tid] = row_off;
             for (int j = 0; j < tl; j++)
-                tiles[tile_off + j] = make_int4(tid, row_off + j * BM, min(BM, tot - j * BM), 0);
+                tiles[tile_off + j] = mtile(tid, row_off, tot, BM, j);
         }
     }
     if (b == 0 && tid == 0) {

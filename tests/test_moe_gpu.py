@@ -422,6 +422,20 @@ def test_forward_fp8_dsv3_t64_full(amd, orc, dsv3):
     assert _fp8_case(amd, orc, dsv3, 64, 256, 8, 7168, 2048, sample=rows) < 2e-2
 
 
+def test_forward_fp8_dsv3_t512_sampled(amd, orc, dsv3):
+    announce("forward_fp8 dsv3 T=512 sampled")
+    rows = np.random.default_rng(5).choice(512, 6, replace=False)
+    assert _fp8_case(amd, orc, dsv3, 512, 256, 8, 7168, 2048, sample=rows) < 2e-2
+
+
+def test_forward_fp8_dsv3_t8192_sampled(amd, orc, dsv3):
+    """BASELINE's largest token count: about half the experts span two
+    (evenly split) M-tiles."""
+    announce("forward_fp8 dsv3 T=8192 sampled")
+    rows = np.random.default_rng(6).choice(8192, 6, replace=False)
+    assert _fp8_case(amd, orc, dsv3, 8192, 256, 8, 7168, 2048, sample=rows) < 2e-2
+
+
 def test_forward_fp8_dsv3_t4096_sampled(amd, orc, dsv3):
     announce("forward_fp8 dsv3 T=4096 sampled")
     rows = np.random.default_rng(4).choice(4096, 6, replace=False)
