@@ -230,6 +230,27 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const int* logical_indices, uint16_t* output,
                                  const DsaConfig* cfg, int pages_per_seq, void* stream);
 
+/* Lightning indexer of DeepSeek-V3.2: the producer of the sparse indices
+ * amdmoe_dsa_decode_bf16_paged consumes.  No counterpart in the reference
+ * (its tests draw the indices at random, tests/test_dsa.cu:73-85); the
+ * formula is the published one, I = sum_j w_j * ReLU(q_j . k), in fp8:
+ *   score[q,s] = k_scale[row] * sum_j head_w[q,j] * q_scale[q,j]
+ *                * relu(q_codes[q,j,:] . k_codes[row,:]),  s < seq_len[q],
+ *   row = page_table[q][s / page] * page + s % page.
+ * q_codes e4m3 [Q,Hi,128], q_scale / head_w fp32 [Q,Hi] (scales > 0);
+ * k_codes e4m3 [cache_rows,128] with k_scale fp32 [cache_rows] (> 0), in
+ * pages of `page` rows; page_table int32 [Q, pages_per_seq]; seq_len int32
+ * [Q] (device).  out int32 [Q, topk]: the topk positions with the largest
+ * scores (ties: the lower position), in ascending position order; a query
+ * with fewer than topk positions lists all of them, then -1.  scores fp32
+ * [Q, max_seq] is caller scratch (left holding the scores, -inf past
+ * seq_len).  Hi in {16, 32, 64, 128}; max_seq <= 32768. */
+int amdmoe_dsa_indexer_topk_fp8(const uint8_t* q_codes, const float* q_scale, const float* head_w,
+                                const uint8_t* k_codes, const float* k_scale, long cache_rows,
+                                const int* page_table, const int* seq_len, int num_queries,
+                                int num_heads, int page, int pages_per_seq, int max_seq, int topk,
+                                float* scores, int* out, void* stream);
+
 /* The reference's DSA stage functions (fp32), same semantics; dsa_forward
  * above does not go through them.  Shapes follow cfg: gathered_kc/v
  * [Q,S,Dc], gathered_kp [Q,S,Dp], scores/attn [Q,H,S], output [Q,H,Dc].

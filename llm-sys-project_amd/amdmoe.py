@@ -23,7 +23,8 @@ SYMBOLS = [
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
     "amdmoe_quant_weight_fp8", "amdmoe_set_stage_events", "amdmoe_dsa_forward_f32",
-    "amdmoe_dsa_decode_bf16_paged", "amdmoe_dsa_kv_gather_f32", "amdmoe_dsa_dot_compressed_f32",
+    "amdmoe_dsa_decode_bf16_paged", "amdmoe_dsa_indexer_topk_fp8", "amdmoe_dsa_kv_gather_f32",
+    "amdmoe_dsa_dot_compressed_f32",
     "amdmoe_dsa_dot_positional_f32", "amdmoe_dsa_dot_fused_f32", "amdmoe_dsa_softmax_f32",
     "amdmoe_dsa_output_proj_f32",
 ]
@@ -86,6 +87,8 @@ def load():
         "amdmoe_set_stage_events": (I, [ctypes.POINTER(_P)]),
         "amdmoe_dsa_forward_f32": (I, [_P, _P, _P, _P, _P, _P, _P, dcfgp, _P]),
         "amdmoe_dsa_decode_bf16_paged": (I, [_P, _P, _P, _P, _P, _P, dcfgp, I, _P]),
+        "amdmoe_dsa_indexer_topk_fp8": (I, [_P, _P, _P, _P, _P, L_, _P, _P, I, I, I, I, I, I,
+                                            _P, _P, _P]),
         "amdmoe_dsa_kv_gather_f32": (I, [_P, _P, _P, _P, _P, _P, _P, dcfgp, _P]),
         "amdmoe_dsa_dot_compressed_f32": (I, [_P, _P, _P, dcfgp, _P]),
         "amdmoe_dsa_dot_positional_f32": (I, [_P, _P, _P, dcfgp, _P]),
@@ -269,6 +272,15 @@ def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, out, cfg, pages_pe
 
 
 # the reference's DSA stage functions (naive_dsa.cuh:31-68)
+def dsa_indexer_topk_fp8(qc, qs, hw, kc, ks, page_table, seq_len, page, max_seq, topk, scores,
+                         out, stream=None):
+    Q, Hi, _ = qc.shape
+    _check(load().amdmoe_dsa_indexer_topk_fp8(_ptr(qc), _ptr(qs), _ptr(hw), _ptr(kc), _ptr(ks),
+                                              kc.shape[0], _ptr(page_table), _ptr(seq_len), Q, Hi,
+                                              page, page_table.shape[1], max_seq, topk,
+                                              _ptr(scores), _ptr(out), _stream(stream)))
+
+
 def dsa_kv_gather_f32(kc, kp, v, idx, gkc, gkp, gv, cfg, stream=None):
     _check(load().amdmoe_dsa_kv_gather_f32(_ptr(kc), _ptr(kp), _ptr(v), _ptr(idx), _ptr(gkc),
                                            _ptr(gkp), _ptr(gv), ctypes.byref(cfg), _stream(stream)))

@@ -482,6 +482,20 @@ static int dsa_cfg_check(const DsaConfig* cfg) {
     return AMDMOE_OK;
 }
 
+int amdmoe_dsa_indexer_topk_fp8(const uint8_t* q_codes, const float* q_scale, const float* head_w,
+                                const uint8_t* k_codes, const float* k_scale, long cache_rows,
+                                const int* page_table, const int* seq_len, int num_queries,
+                                int num_heads, int page, int pages_per_seq, int max_seq, int topk,
+                                float* scores, int* out, void* stream) {
+    AMDMOE_CHECK_ARG(num_queries >= 0, "dsa_indexer: num_queries=%d", num_queries);
+    AMDMOE_CHECK_ARG(q_codes && q_scale && head_w && k_codes && k_scale && page_table && seq_len &&
+                         scores && out,
+                     "null tensor pointer");
+    return launch_dsa_indexer(q_codes, q_scale, head_w, k_codes, cache_rows, k_scale, page_table,
+                              seq_len, num_queries, num_heads, page, pages_per_seq, max_seq, topk,
+                              scores, out, (hipStream_t)stream);
+}
+
 int amdmoe_dsa_kv_gather_f32(const float* kv_cache_compressed, const float* kv_cache_positional,
                              const float* v_cache, const int* sparse_indices, float* gathered_kc,
                              float* gathered_kp, float* gathered_v, const DsaConfig* cfg,

@@ -1,0 +1,258 @@
+// DeepSeek-V3.2's lightning indexer: the producer of the sparse indices the
+// DSA decode consumes.  The reference has no indexer (its tests draw the
+// indices at random, tests/test_dsa.cu:73-85); the formula is the published
+// one, I[t,s] = sum_j w[t,j] * ReLU(q[t,j] . k[s]), in fp8:
+//   score[q,s] = ks[row] * sum_j (hw[q,j] * qs[q,j]) * relu(q8[q,j,:] . k8[row,:])
+//   row = page_table[q][s / page] * page + s % page,  s < seq_len[q]
+// (the positive scales ks and qs commute with the ReLU), then the topk
+// positions per query by score, ties to the lower position, listed in
+// ascending position order -- the logical indices dsa_decode_bf16_paged takes.
+//
+// indexer_scores_kernel: one workgroup per (query, 256 positions), 4 waves
+//   of 64 positions.  Per 16-position tile one fp8 MFMA per 16 heads,
+//   S (16 positions x 16 heads) = K8 . Q8^T, keys as operand A straight from
+//   the paged cache (two 16-byte loads per lane, a 128-byte row per 4
+//   lanes), the query's heads as operand B held in registers.  Each lane
+//   folds ReLU and the head weight over its heads, a 16-lane butterfly sums
+//   the heads; HBM-bound on the keys (128 bytes + a 4-byte scale per
+//   position).
+// indexer_topk_kernel: one 1024-thread workgroup per query.  The scores
+//   become order-preserving 32-bit keys in LDS (128 KB at 32768 positions);
+//   a most-significant-digit-first radix select (four 8-bit passes, LDS
+//   histograms) finds the key of the topk-th largest score and how many
+//   positions holding exactly it are taken; two block scans then write the
+//   selected positions in ascending order.
+#include "internal.hpp"
+
+namespace amdmoe {
+
+constexpr int kIdxD = 128;         // index head dim (bytes per fp8 row)
+constexpr int kIdxMaxHeads = 128;  // index heads, a multiple of 16
+constexpr int kIdxTile = 256;      // positions per workgroup of the scoring kernel
+constexpr int kIdxMaxSeq = 32768;  // positions per query of the selection kernel
+constexpr int kTopkThreads = 1024;
+
+template <int HT>  // head tiles of 16
+__global__ __launch_bounds__(256) void indexer_scores_kernel(
+    const uint8_t* __restrict__ qc, const float* __restrict__ qs, const float* __restrict__ hw,
+    const uint8_t* __restrict__ kc, long kc_bytes, const float* __restrict__ ks,
+    const int* __restrict__ page_table, const int* __restrict__ seq_len, int Q, int page,
+    int pages_per_seq, int max_seq, int ntile, float* __restrict__ scores) {
+    const int qi = blockIdx.x / ntile, tb = blockIdx.x - qi * ntile;
+    if (qi >= Q) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int len = min(seq_len[qi], max_seq);
+    const long seq = (long)pages_per_seq * page;
+    constexpr int Hi = 16 * HT;
+
+    // the query's heads as B operands: head 16h + r16, bytes 16g.. and 64+16g..
+    i32x8 qf[HT];
+    float wq[HT];
+#pragma unroll
+    for (int h = 0; h < HT; h++) {
+        const uint8_t* qr = qc + ((size_t)qi * Hi + 16 * h + r16) * kIdxD;
+        const u32x4 lo = *(const u32x4*)(qr + 16 * g), hi = *(const u32x4*)(qr + 64 + 16 * g);
+        qf[h] = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        const size_t hq = (size_t)qi * Hi + 16 * h + r16;
+        wq[h] = hw[hq] * qs[hq];
+    }
+
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc, kc_bytes);
+    const int* pt = page_table + (size_t)qi * pages_per_seq;
+    // this wave's 4 tiles of 16 positions: keys (operand A) and scales
+    constexpr int kTiles = 4;
+    i32x8 kf[kTiles];
+    float ksc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; t++) {
+        const int s = tb * kIdxTile + 64 * wave + 16 * t + r16;
+        long row = -1;
+        if (s < len) {
+            const int p = pt[s / page];
+            row = (long)p * page + s % page;
+            if (p < 0 || row < 0 || (long)s >= seq) row = -1;
+        }
+        const uint32_t vo = row >= 0 && (row + 1) * kIdxD <= kc_bytes ? (uint32_t)(row * kIdxD + 16 * g) : kOob;
+        const u32x4 lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0));
+        const u32x4 hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 64, 0));
+        kf[t] = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        ksc[t] = row >= 0 ? ks[row] : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; t++) {
+        // lane (g, r16) holds S[4g + i][r16]: positions 4g + i of the tile, head r16
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < HT; h++) {
+            const f32x4 c = mfma_fp8(kf[t], qf[h], (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] += wq[h] * fmaxf(c[i], 0.0f);
+        }
+        // sum over the 16 heads of each head tile: butterfly within 16 lanes
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] += __shfl_xor(v[i], o, 16);
+        // lane (g, n < 4) writes position 4g + n with the scale of its row,
+        // held by the lane that loaded that row (r16 = 4g + n)
+        const int n = r16 & 3;
+        const float sc = __shfl(ksc[t], 4 * g + n, 64);
+        const float tot = n == 0 ? v[0] : (n == 1 ? v[1] : (n == 2 ? v[2] : v[3]));
+        const int s = tb * kIdxTile + 64 * wave + 16 * t + 4 * g + n;
+        if (r16 < 4 && s < max_seq) scores[(size_t)qi * max_seq + s] = s < len ? tot * sc : -INFINITY;
+    }
+}
+
+// order-preserving key of a score (larger score, larger key; -0 as +0)
+__device__ __forceinline__ uint32_t score_key(float f) {
+    if (f == 0.0f) f = 0.0f;
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// exclusive block scan of one int per thread (1024 threads)
+__device__ __forceinline__ int block_excl_scan(int v, int* s_wave, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int w = 0; w < kTopkThreads / 64; w++) {
+        if (w < wave) before += s_wave[w];
+        all += s_wave[w];
+    }
+    __syncthreads();
+    *total = all;
+    return before + x - v;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float* __restrict__ scores,
+                                                                    const int* __restrict__ seq_len,
+                                                                    int max_seq, int topk,
+                                                                    int* __restrict__ out) {
+    extern __shared__ uint32_t s_key[];  // [max_seq]
+    __shared__ int s_hist[256];
+    __shared__ int s_wave[kTopkThreads / 64];
+    __shared__ uint32_t s_sel[2];        // digit, remaining count
+    const int qi = blockIdx.x, tid = threadIdx.x;
+    const int n = min(seq_len[qi], max_seq);
+    const float* row = scores + (size_t)qi * max_seq;
+    for (int s = tid; s < max_seq; s += kTopkThreads) s_key[s] = s < n ? score_key(row[s]) : 0u;
+    __syncthreads();
+
+    // radix select of the topk-th largest key among the n valid positions
+    uint32_t prefix = 0, mask = 0;
+    int need = min(topk, n);
+    const bool all = n <= topk;
+    if (!all) {
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            if (tid < 256) s_hist[tid] = 0;
+            __syncthreads();
+            for (int s = tid; s < n; s += kTopkThreads) {
+                const uint32_t k = s_key[s];
+                if ((k & mask) == prefix) atomicAdd(&s_hist[(k >> shift) & 0xff], 1);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, d = 255;
+                for (; d > 0; d--) {
+                    if (cum + s_hist[d] >= need) break;
+                    cum += s_hist[d];
+                }
+                s_sel[0] = (uint32_t)d;
+                s_sel[1] = (uint32_t)(need - cum);
+            }
+            __syncthreads();
+            prefix |= s_sel[0] << shift;
+            mask |= 0xffu << shift;
+            need = (int)s_sel[1];
+            __syncthreads();
+        }
+    }
+    // prefix = the threshold key; positions above it are all taken, and the
+    // first `need` positions equal to it
+    constexpr int kPer = kIdxMaxSeq / kTopkThreads;  // 32 consecutive positions per thread
+    const int s0 = tid * kPer;
+    int n_eq = 0;
+    for (int j = 0; j < kPer; j++) {
+        const int s = s0 + j;
+        if (s < n && !all && s_key[s] == prefix) n_eq++;
+    }
+    int tmp;
+    const int eq_before = block_excl_scan(n_eq, s_wave, &tmp);
+    int n_sel = 0;
+    {
+        int eq = eq_before;
+        for (int j = 0; j < kPer; j++) {
+            const int s = s0 + j;
+            if (s >= n) break;
+            const uint32_t k = s_key[s];
+            if (all || k > prefix) n_sel++;
+            else if (k == prefix && eq++ < need) n_sel++;
+        }
+    }
+    int total;
+    int pos = block_excl_scan(n_sel, s_wave, &total);
+    {
+        int eq = eq_before;
+        int* o = out + (size_t)qi * topk;
+        for (int j = 0; j < kPer; j++) {
+            const int s = s0 + j;
+            if (s >= n) break;
+            const uint32_t k = s_key[s];
+            bool take = all || k > prefix;
+            if (!take && k == prefix) take = eq++ < need;
+            if (take) o[pos++] = s;
+        }
+        for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
+    }
+}
+
+int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
+                       long kc_rows, const float* ks, const int* page_table, const int* seq_len,
+                       int Q, int Hi, int page, int pages_per_seq, int max_seq, int topk,
+                       float* scores, int* out, hipStream_t st) {
+    AMDMOE_CHECK_ARG(Hi >= 16 && Hi <= kIdxMaxHeads && Hi % 16 == 0,
+                     "dsa_indexer: Hi=%d must be a multiple of 16 in [16, %d]", Hi, kIdxMaxHeads);
+    AMDMOE_CHECK_ARG(max_seq >= 1 && max_seq <= kIdxMaxSeq, "dsa_indexer: max_seq=%d outside [1, %d]",
+                     max_seq, kIdxMaxSeq);
+    AMDMOE_CHECK_ARG(topk >= 1 && page >= 1 && pages_per_seq >= 1 && kc_rows >= 1,
+                     "dsa_indexer: bad topk / paging");
+    AMDMOE_CHECK_ARG(kc_rows * kIdxD < 0x7FFFFFF0L, "dsa_indexer: key cache of %ld rows exceeds 2 GiB", kc_rows);
+    if (Q == 0) return AMDMOE_OK;
+    const int ntile = (max_seq + kIdxTile - 1) / kIdxTile;
+    const long grid = (long)Q * ntile;
+    AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_indexer: grid too large");
+    const long kb = kc_rows * kIdxD;
+#define AMDMOE_IDX_LAUNCH(HT)                                                                        \
+    hipLaunchKernelGGL(indexer_scores_kernel<HT>, dim3((unsigned)grid), dim3(256), 0, st, qc, qs, hw, \
+                       kc, kb, ks, page_table, seq_len, Q, page, pages_per_seq, max_seq, ntile, scores)
+    switch (Hi / 16) {
+        case 1: AMDMOE_IDX_LAUNCH(1); break;
+        case 2: AMDMOE_IDX_LAUNCH(2); break;
+        case 4: AMDMOE_IDX_LAUNCH(4); break;
+        case 8: AMDMOE_IDX_LAUNCH(8); break;
+        default: return set_error(AMDMOE_ERR_INVALID, "dsa_indexer: Hi=%d must be 16, 32, 64 or 128", Hi);
+    }
+#undef AMDMOE_IDX_LAUNCH
+    AMDMOE_LAUNCH_CHECK();
+    static bool attr_set = false;
+    if (!attr_set) {
+        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)indexer_topk_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kIdxMaxSeq * 4));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(indexer_topk_kernel, dim3((unsigned)Q), dim3(kTopkThreads), (size_t)max_seq * 4,
+                       st, scores, seq_len, max_seq, topk, out);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
+}  // namespace amdmoe

@@ -89,6 +89,12 @@ int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const floa
 // scratch: dsa_paged_scratch_bytes(Q, H, S) bytes (split partials), may be
 // 0 bytes / nullptr when that is 0
 size_t dsa_paged_scratch_bytes(int Q, int H, int S);
+// dsa_indexer.hip: lightning-indexer scores [Q, max_seq] (scratch) and the
+// topk positions per query
+int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
+                       long kc_rows, const float* ks, const int* page_table, const int* seq_len,
+                       int Q, int Hi, int page, int pages_per_seq, int max_seq, int topk,
+                       float* scores, int* out, hipStream_t st);
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
                           long cache_tokens, const int* page_table, const int* logical,
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,

@@ -76,3 +76,26 @@ def dsa_paged(Q, H, Dc, Dp, S, page, ctx, seed=5, device="cuda"):
     qn = torch.randn((Q, H, Dc), generator=g, device=device).to(torch.bfloat16)
     qp = torch.randn((Q, H, Dp), generator=g, device=device).to(torch.bfloat16)
     return (qn.view(torch.int16), qp.view(torch.int16), cache.view(torch.int16), pt, logical, pps)
+
+
+def dsa_indexer(Q, Hi, ctx, page, seed=9, page_table=None, device="cuda"):
+    """Lightning-indexer inputs: fp8 e4m3 query heads [Q,Hi,128] and keys
+    [Q*ctx,128] (paged like the latent cache), each row quantised with one
+    fp32 scale (amdmoe_quant_rows_fp8: amax/448), per-head weights
+    ~ N(0, 1/Hi), and a page table (a random permutation of all pages unless
+    one is given)."""
+    g = _gen(seed, device)
+    pps = ctx // page
+    q = torch.randn((Q * Hi, 128), generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn((Q * ctx, 128), generator=g, device=device).to(torch.bfloat16)
+    qc = torch.empty((Q * Hi, 128), dtype=torch.uint8, device=device)
+    qs = torch.empty((Q * Hi, 1), dtype=torch.float32, device=device)
+    kc = torch.empty((Q * ctx, 128), dtype=torch.uint8, device=device)
+    ks = torch.empty((Q * ctx, 1), dtype=torch.float32, device=device)
+    amdmoe.quant_rows_fp8(q.view(torch.int16), qc, qs)
+    amdmoe.quant_rows_fp8(k.view(torch.int16), kc, ks)
+    hw = torch.randn((Q, Hi), generator=g, device=device) * (1.0 / Hi ** 0.5)
+    if page_table is None:
+        page_table = torch.randperm(Q * pps, generator=g, device=device).to(torch.int32).reshape(Q, pps)
+    return (qc.reshape(Q, Hi, 128), qs.reshape(Q, Hi), hw.contiguous(), kc, ks.reshape(Q * ctx),
+            page_table)

@@ -69,6 +69,9 @@ def lib():
             "orc_dsa_translate": (None, [_i32p, _i32p, _I, _I, _I, _I, _i32p]),
             "orc_dsa_decode_bf16_paged": (None, [_u16p, _u16p, _u16p, _i32p, _i32p, _f32p,
                                                  _I, _I, _I, _I, _I, _I, _I]),
+            "orc_dsa_indexer_scores": (None, [_u8p, _f32p, _f32p, _u8p, _f32p, _i32p, _i32p,
+                                              _I, _I, _I, _I, _I, _f32p]),
+            "orc_dsa_indexer_topk": (None, [_f32p, _i32p, _I, _I, _I, _i32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -344,4 +347,29 @@ def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, Dc, page):
     out = np.empty((Q, H, Dc), np.float32)
     lib().orc_dsa_decode_bf16_paged(qn, qp, cache, pt, logical, out, Q, H, Dc, Dp, S,
                                     pt.shape[1], page)
+    return out
+
+
+# ---------------------------------------------------------------- indexer
+def dsa_indexer_scores(qc, qs, hw, kc, ks, page_table, seq_len, page, max_seq):
+    """Lightning-indexer scores (double precision, rounded once to fp32):
+    score[q,s] = ks[row] * sum_j hw[q,j] qs[q,j] relu(q[q,j,:] . k[row,:]),
+    -inf past seq_len[q]."""
+    qc, kc = _c(qc, np.uint8), _c(kc, np.uint8)
+    qs, hw, ks = (_c(a, np.float32) for a in (qs, hw, ks))
+    pt, sl = _c(page_table, np.int32), _c(seq_len, np.int32)
+    Q, Hi, _ = qc.shape
+    out = np.empty((Q, max_seq), np.float32)
+    lib().orc_dsa_indexer_scores(qc, qs, hw, kc, ks, pt, sl, Q, Hi, page, pt.shape[1], max_seq, out)
+    return out
+
+
+def dsa_indexer_topk(scores, seq_len, topk):
+    """The topk positions per row by score (ties: lower position), in
+    ascending position order, padded with -1."""
+    scores = _c(scores, np.float32)
+    sl = _c(seq_len, np.int32)
+    Q, max_seq = scores.shape
+    out = np.empty((Q, topk), np.int32)
+    lib().orc_dsa_indexer_topk(scores, sl, Q, max_seq, topk, out)
     return out

@@ -647,3 +647,70 @@ EXPORT void orc_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_
         free(kc); free(kp); free(scores); free(qn); free(qp);
     }
 }
+
+/* ------------------------------------------------------------------ indexer
+ * DeepSeek-V3.2's lightning indexer, the producer of the sparse indices the
+ * decode consumes (absent from the reference; the formula is the published
+ * one, I[t,s] = sum_j w[t,j] * ReLU(q[t,j] . k[s])), in the fp8 form the
+ * library takes: q codes e4m3 [Q,Hi,128] with scales [Q,Hi], per-head
+ * weights [Q,Hi], key codes e4m3 [rows,128] with a scale per row, keys in
+ * pages through page_table.  Scores are computed in double and rounded once:
+ *   score[q,s] = ks[row] * sum_j (w[q,j] * qs[q,j]) * relu(sum_d q[q,j,d] k[row,d])
+ * for s < seq_len[q]; row = page_table[q][s / page] * page + s % page. */
+EXPORT void orc_dsa_indexer_scores(const uint8_t* qc, const float* qs, const float* hw,
+                                   const uint8_t* kc, const float* ks, const int* page_table,
+                                   const int* seq_len, int Q, int Hi, int page, int pages_per_seq,
+                                   int max_seq, float* scores) {
+    #pragma omp parallel for schedule(dynamic)
+    for (int q = 0; q < Q; q++) {
+        float qf[128];
+        double* wq = (double*)malloc(sizeof(double) * (size_t)Hi);
+        float* qv = (float*)malloc(sizeof(float) * (size_t)Hi * 128);
+        for (int j = 0; j < Hi; j++) {
+            wq[j] = (double)hw[(size_t)q * Hi + j] * (double)qs[(size_t)q * Hi + j];
+            for (int d = 0; d < 128; d++) qv[(size_t)j * 128 + d] = orc_e4m3_to_f32(qc[((size_t)q * Hi + j) * 128 + d]);
+        }
+        for (int s = 0; s < max_seq; s++) {
+            if (s >= seq_len[q]) { scores[(size_t)q * max_seq + s] = -INFINITY; continue; }
+            long row = (long)page_table[(size_t)q * pages_per_seq + s / page] * page + s % page;
+            for (int d = 0; d < 128; d++) qf[d] = orc_e4m3_to_f32(kc[row * 128 + d]);
+            double tot = 0.0;
+            for (int j = 0; j < Hi; j++) {
+                double dot = 0.0;
+                for (int d = 0; d < 128; d++) dot += (double)qv[(size_t)j * 128 + d] * (double)qf[d];
+                tot += wq[j] * (dot > 0.0 ? dot : 0.0);
+            }
+            scores[(size_t)q * max_seq + s] = (float)(tot * (double)ks[row]);
+        }
+        free(wq);
+        free(qv);
+    }
+}
+
+/* The topk positions of each row with the largest scores (ties: the lower
+ * position wins; -0 equals +0), listed in ascending position order; rows
+ * shorter than topk are padded with -1. */
+static int g_topk_len;
+static const float* g_topk_row;
+static int cmp_score_desc(const void* a, const void* b) {
+    int i = *(const int*)a, j = *(const int*)b;
+    float x = g_topk_row[i], y = g_topk_row[j];
+    if (x > y) return -1;
+    if (x < y) return 1;
+    return i - j;
+}
+EXPORT void orc_dsa_indexer_topk(const float* scores, const int* seq_len, int Q, int max_seq,
+                                 int topk, int* out) {
+    int* pos = (int*)malloc(sizeof(int) * (size_t)(max_seq > 0 ? max_seq : 1));
+    for (int q = 0; q < Q; q++) {
+        int n = seq_len[q] < max_seq ? seq_len[q] : max_seq;
+        for (int s = 0; s < n; s++) pos[s] = s;
+        g_topk_row = scores + (size_t)q * max_seq;
+        g_topk_len = n;
+        qsort(pos, (size_t)n, sizeof(int), cmp_score_desc);
+        int m = n < topk ? n : topk;
+        qsort(pos, (size_t)m, sizeof(int), cmp_int);
+        for (int k = 0; k < topk; k++) out[(size_t)q * topk + k] = k < m ? pos[k] : -1;
+    }
+    free(pos);
+}
