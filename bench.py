@@ -98,6 +98,28 @@ def dsa_bench(amdmoe, synth, iters=20):
             "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
 
 
+def indexer_bench(amdmoe, synth, iters=20):
+    """Lightning indexer at the decode shape: 64 queries, 64 fp8 index heads,
+    32768 positions each, top-2048 (the indices dsa_decode consumes)."""
+    import torch
+    Q, Hi, ctx, page, topk = 64, 64, 32768, 64, 2048
+    qc, qs, hw, kc, ks, pt = synth.dsa_indexer(Q, Hi, ctx, page, seed=41)
+    sl = torch.full((Q,), ctx, dtype=torch.int32, device="cuda")
+    scores = torch.empty((Q, ctx), dtype=torch.float32, device="cuda")
+    out = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    ms = _time_calls(lambda: amdmoe.dsa_indexer_topk_fp8(qc, qs, hw, kc, ks, pt, sl, page, ctx, topk,
+                                                        scores, out), iters)
+    # keys + their scales once, q and head data, scores written and read back, indices
+    nbytes = Q * ctx * (128 + 4) + Q * Hi * (128 + 8) + Q * (ctx // page) * 4 + 2 * Q * ctx * 4 + Q * topk * 4
+    flops = 2 * Q * ctx * Hi * 128
+    del qc, qs, hw, kc, ks, pt, scores, out
+    return {"us_per_call": round(ms * 1e3, 2), "queries_per_s": round(Q / (ms * 1e-3), 1),
+            "hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
+            "fp8_mfma_frac": round(flops / (ms * 1e-3) / FP8_PEAK, 4),
+            "shape": f"Q={Q} Hi={Hi} ctx={ctx} top-{topk}"}
+
+
 def _time_calls(fn, iters, warmup=3):
     """Mean ms of fn() over iters calls, hip events on torch's current stream
     (the stream every amdmoe wrapper launches on by default)."""
@@ -404,6 +426,8 @@ def main():
     torch.cuda.set_device(0)
     if args.sweep:
         rows = sweep(amdmoe, synth, args.steps)
+        ix = indexer_bench(amdmoe, synth)
+        log(f"[sweep] dsa indexer: {ix}")
         rows.append({"config": "dsa_decode_B64_H128_S2048", **dsa_bench(amdmoe, synth)})
         log(f"[sweep] dsa: {rows[-1]}")
         with open(args.sweep, "w") as f:
@@ -418,6 +442,9 @@ def main():
         md.append(f"| {d['config']} (bf16, paged) | {d['us_per_call'] / 1e3:.4f} | "
                   f"{d['queries_per_s']:.0f} queries/s | {100 * d['bf16_mfma_frac']:.1f}% of bf16 | | "
                   f"{0.0212:.4f} | {100 * d['hbm_frac']:.1f}% of HBM peak |")
+        md.append(f"| dsa_indexer ({ix['shape']}, fp8) | {ix['us_per_call'] / 1e3:.4f} | "
+                  f"{ix['queries_per_s']:.0f} queries/s | {100 * ix['fp8_mfma_frac']:.1f}% of fp8 | | | "
+                  f"{100 * ix['hbm_frac']:.1f}% of HBM peak |")
         with open(os.path.splitext(args.sweep)[0] + ".md", "w") as f:
             f.write("\n".join(md) + "\n")
         return
@@ -519,6 +546,8 @@ def main():
     if not args.skip_dsa:
         log("[bench] DSA decode")
         result["dsa_decode"] = dsa_bench(amdmoe, synth)
+        log("[bench] DSA indexer")
+        result["dsa_indexer"] = indexer_bench(amdmoe, synth)
     if args.cpu_sample > 0:
         log(f"[bench] CPU baseline on {args.cpu_sample} tokens")
         result["cpu_baseline"] = cpu_baseline(x, wg, w1q, w1s, w2q, w2s, K, args.cpu_sample)

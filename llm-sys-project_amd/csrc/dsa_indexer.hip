@@ -16,12 +16,17 @@
 //   folds ReLU and the head weight over its heads, a 16-lane butterfly sums
 //   the heads; HBM-bound on the keys (128 bytes + a 4-byte scale per
 //   position).
-// indexer_topk_kernel: one 1024-thread workgroup per query.  The scores
-//   become order-preserving 32-bit keys in LDS (128 KB at 32768 positions);
-//   a most-significant-digit-first radix select (four 8-bit passes, LDS
-//   histograms) finds the key of the topk-th largest score and how many
-//   positions holding exactly it are taken; two block scans then write the
-//   selected positions in ascending order.
+// indexer_topk_kernel: one 1024-thread workgroup per query, 32 positions
+//   per thread held in registers as order-preserving 32-bit keys.  A
+//   most-significant-digit-first radix select (four 8-bit passes) finds the
+//   key of the topk-th largest score and how many positions holding exactly
+//   it are taken.  For the histogram passes a thread holds positions
+//   tid, tid + 1024, ... and each wave counts into its own LDS histogram, so
+//   one atomic instruction covers 64 unrelated positions (a shared
+//   histogram with consecutive positions serialised on the few leading
+//   digits real scores have: 111 us per query batch).  The selection then
+//   takes 32 consecutive positions per thread and two block scans write
+//   them in ascending order.
 #include "internal.hpp"
 
 namespace amdmoe {
@@ -137,15 +142,23 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
                                                                     const int* __restrict__ seq_len,
                                                                     int max_seq, int topk,
                                                                     int* __restrict__ out) {
-    extern __shared__ uint32_t s_key[];  // [max_seq]
-    __shared__ int s_hist[256];
-    __shared__ int s_wave[kTopkThreads / 64];
-    __shared__ uint32_t s_sel[2];        // digit, remaining count
-    const int qi = blockIdx.x, tid = threadIdx.x;
+    constexpr int kPer = kIdxMaxSeq / kTopkThreads;  // 32 consecutive positions per thread
+    constexpr int kWaves = kTopkThreads / 64;
+    __shared__ int s_hist[kWaves][256];              // one histogram per wave
+    __shared__ int s_tot[256];
+    __shared__ int s_wave[kWaves];
+    __shared__ uint32_t s_sel[2];                    // digit, remaining count
+    const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = min(seq_len[qi], max_seq);
     const float* row = scores + (size_t)qi * max_seq;
-    for (int s = tid; s < max_seq; s += kTopkThreads) s_key[s] = s < n ? score_key(row[s]) : 0u;
-    __syncthreads();
+    // histogram passes: position j * 1024 + tid in key[j], so the 64 lanes
+    // of a wave hold 64 unrelated positions and their atomics rarely meet
+    uint32_t key[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int s = j * kTopkThreads + tid;
+        key[j] = s < n ? score_key(row[s]) : 0u;
+    }
 
     // radix select of the topk-th largest key among the n valid positions
     uint32_t prefix = 0, mask = 0;
@@ -153,18 +166,24 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     const bool all = n <= topk;
     if (!all) {
         for (int shift = 24; shift >= 0; shift -= 8) {
-            if (tid < 256) s_hist[tid] = 0;
+            for (int i = tid; i < kWaves * 256; i += kTopkThreads) (&s_hist[0][0])[i] = 0;
             __syncthreads();
-            for (int s = tid; s < n; s += kTopkThreads) {
-                const uint32_t k = s_key[s];
-                if ((k & mask) == prefix) atomicAdd(&s_hist[(k >> shift) & 0xff], 1);
+#pragma unroll
+            for (int j = 0; j < kPer; j++)
+                if (j * kTopkThreads + tid < n && (key[j] & mask) == prefix)
+                    atomicAdd(&s_hist[wave][(key[j] >> shift) & 0xff], 1);
+            __syncthreads();
+            if (tid < 256) {
+                int t = 0;
+                for (int w = 0; w < kWaves; w++) t += s_hist[w][tid];
+                s_tot[tid] = t;
             }
             __syncthreads();
             if (tid == 0) {
                 int cum = 0, d = 255;
                 for (; d > 0; d--) {
-                    if (cum + s_hist[d] >= need) break;
-                    cum += s_hist[d];
+                    if (cum + s_tot[d] >= need) break;
+                    cum += s_tot[d];
                 }
                 s_sel[0] = (uint32_t)d;
                 s_sel[1] = (uint32_t)(need - cum);
@@ -176,26 +195,30 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
             __syncthreads();
         }
     }
-    // prefix = the threshold key; positions above it are all taken, and the
-    // first `need` positions equal to it
-    constexpr int kPer = kIdxMaxSeq / kTopkThreads;  // 32 consecutive positions per thread
+    // selection in position order: 32 consecutive positions per thread,
+    // their keys read again (the row is in L2)
     const int s0 = tid * kPer;
-    int n_eq = 0;
+#pragma unroll
     for (int j = 0; j < kPer; j++) {
         const int s = s0 + j;
-        if (s < n && !all && s_key[s] == prefix) n_eq++;
+        key[j] = s < n ? score_key(row[s]) : 0u;
     }
+    // prefix = the threshold key; positions above it are all taken, and the
+    // first `need` positions equal to it
+    int n_eq = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; j++) n_eq += (s0 + j < n && !all && key[j] == prefix) ? 1 : 0;
     int tmp;
     const int eq_before = block_excl_scan(n_eq, s_wave, &tmp);
     int n_sel = 0;
     {
         int eq = eq_before;
+#pragma unroll
         for (int j = 0; j < kPer; j++) {
-            const int s = s0 + j;
-            if (s >= n) break;
-            const uint32_t k = s_key[s];
-            if (all || k > prefix) n_sel++;
-            else if (k == prefix && eq++ < need) n_sel++;
+            const bool valid = s0 + j < n;
+            bool take = valid && (all || key[j] > prefix);
+            if (valid && !take && key[j] == prefix) take = eq++ < need;
+            n_sel += take ? 1 : 0;
         }
     }
     int total;
@@ -203,13 +226,12 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     {
         int eq = eq_before;
         int* o = out + (size_t)qi * topk;
+#pragma unroll
         for (int j = 0; j < kPer; j++) {
-            const int s = s0 + j;
-            if (s >= n) break;
-            const uint32_t k = s_key[s];
-            bool take = all || k > prefix;
-            if (!take && k == prefix) take = eq++ < need;
-            if (take) o[pos++] = s;
+            const bool valid = s0 + j < n;
+            bool take = valid && (all || key[j] > prefix);
+            if (valid && !take && key[j] == prefix) take = eq++ < need;
+            if (take) o[pos++] = s0 + j;
         }
         for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
     }
@@ -243,14 +265,8 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
     }
 #undef AMDMOE_IDX_LAUNCH
     AMDMOE_LAUNCH_CHECK();
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)indexer_topk_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kIdxMaxSeq * 4));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(indexer_topk_kernel, dim3((unsigned)Q), dim3(kTopkThreads), (size_t)max_seq * 4,
-                       st, scores, seq_len, max_seq, topk, out);
+    hipLaunchKernelGGL(indexer_topk_kernel, dim3((unsigned)Q), dim3(kTopkThreads), 0, st, scores,
+                       seq_len, max_seq, topk, out);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
