@@ -24,9 +24,10 @@
 //   tid, tid + 1024, ... and each wave counts into its own LDS histogram, so
 //   one atomic instruction covers 64 unrelated positions (a shared
 //   histogram with consecutive positions serialised on the few leading
-//   digits real scores have: 111 us per query batch).  The selection then
-//   takes 32 consecutive positions per thread and two block scans write
-//   them in ascending order.
+//   digits real scores have).  Wave 0 then finds the digit with a suffix
+//   scan across its lanes (4 digits per lane).  The selection takes
+//   ceil(n / 1024) consecutive positions per thread, and one block scan of
+//   the packed (greater, equal) counts places them in ascending order.
 #include "internal.hpp"
 
 namespace amdmoe {
@@ -138,21 +139,20 @@ __device__ __forceinline__ int block_excl_scan(int v, int* s_wave, int* total) {
     return before + x - v;
 }
 
+template <int kPer>  // positions per thread: max_seq <= 1024 * kPer
 __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float* __restrict__ scores,
                                                                     const int* __restrict__ seq_len,
                                                                     int max_seq, int topk,
                                                                     int* __restrict__ out) {
-    constexpr int kPer = kIdxMaxSeq / kTopkThreads;  // 32 consecutive positions per thread
     constexpr int kWaves = kTopkThreads / 64;
-    __shared__ int s_hist[kWaves][256];              // one histogram per wave
-    __shared__ int s_tot[256];
+    __shared__ __align__(16) int s_hist[kWaves][256];  // one histogram per wave
     __shared__ int s_wave[kWaves];
-    __shared__ uint32_t s_sel[2];                    // digit, remaining count
+    __shared__ int s_sel[2];                           // digit, remaining count
     const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = min(seq_len[qi], max_seq);
     const float* row = scores + (size_t)qi * max_seq;
     // histogram passes: position j * 1024 + tid in key[j], so the 64 lanes
-    // of a wave hold 64 unrelated positions and their atomics rarely meet
+    // of a wave hold 64 unrelated positions
     uint32_t key[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
@@ -165,76 +165,91 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     int need = min(topk, n);
     const bool all = n <= topk;
     if (!all) {
+        for (int i = tid; i < kWaves * 256; i += kTopkThreads) (&s_hist[0][0])[i] = 0;
+        __syncthreads();
         for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = tid; i < kWaves * 256; i += kTopkThreads) (&s_hist[0][0])[i] = 0;
-            __syncthreads();
 #pragma unroll
             for (int j = 0; j < kPer; j++)
                 if (j * kTopkThreads + tid < n && (key[j] & mask) == prefix)
                     atomicAdd(&s_hist[wave][(key[j] >> shift) & 0xff], 1);
             __syncthreads();
-            if (tid < 256) {
-                int t = 0;
-                for (int w = 0; w < kWaves; w++) t += s_hist[w][tid];
-                s_tot[tid] = t;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                int cum = 0, d = 255;
-                for (; d > 0; d--) {
-                    if (cum + s_tot[d] >= need) break;
-                    cum += s_tot[d];
+            if (wave == 0) {
+                // lane l owns digits 4l..4l+3: their counts over all waves,
+                // zeroed behind it for the next pass
+                int c[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) {
+                    int4* h = (int4*)&s_hist[w][4 * lane];
+                    const int4 v = *h;
+                    c[0] += v.x; c[1] += v.y; c[2] += v.z; c[3] += v.w;
+                    *h = make_int4(0, 0, 0, 0);
                 }
-                s_sel[0] = (uint32_t)d;
-                s_sel[1] = (uint32_t)(need - cum);
+                // count of keys with digit >= 4l + i: this lane's suffix plus
+                // every higher lane's total
+                const int s3 = c[3], s2 = s3 + c[2], s1 = s2 + c[1], s0 = s1 + c[0];
+                int x = s0;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int y = __shfl_down(x, o, 64);
+                    if (lane + o < 64) x += y;
+                }
+                const int above = x - s0;
+                const int ge[4] = {above + s0, above + s1, above + s2, above + s3};
+                // the digit is the largest d whose count of keys >= d reaches
+                // need; the counts fall with d, so it is the number of such
+                // digits minus one (digit 0 if none)
+                int cnt = (ge[0] >= need) + (ge[1] >= need) + (ge[2] >= need) + (ge[3] >= need);
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+                const int d = max(cnt - 1, 0);
+                if (lane == (d >> 2)) {
+                    const int i = d & 3;
+                    const int ge_d = i == 0 ? ge[0] : (i == 1 ? ge[1] : (i == 2 ? ge[2] : ge[3]));
+                    const int cd = i == 0 ? c[0] : (i == 1 ? c[1] : (i == 2 ? c[2] : c[3]));
+                    s_sel[0] = d;
+                    s_sel[1] = need - (ge_d - cd);
+                }
             }
             __syncthreads();
-            prefix |= s_sel[0] << shift;
+            prefix |= (uint32_t)s_sel[0] << shift;
             mask |= 0xffu << shift;
-            need = (int)s_sel[1];
-            __syncthreads();
+            need = s_sel[1];
         }
     }
-    // selection in position order: 32 consecutive positions per thread,
-    // their keys read again (the row is in L2)
-    const int s0 = tid * kPer;
+    // prefix = the threshold key; positions above it are all taken, and the
+    // first `need` positions equal to it.  Selection in position order:
+    // thread tid takes the `per` consecutive positions from tid * per, their
+    // keys read again (the row is in L2)
+    const int per = (n + kTopkThreads - 1) / kTopkThreads;
+    const int s0 = tid * per;
+    int n_gt = 0, n_eq = 0;
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
         const int s = s0 + j;
-        key[j] = s < n ? score_key(row[s]) : 0u;
+        key[j] = j < per && s < n ? score_key(row[s]) : 0u;
+        const bool valid = j < per && s < n;
+        n_gt += valid && (all || key[j] > prefix) ? 1 : 0;
+        n_eq += valid && !all && key[j] == prefix ? 1 : 0;
     }
-    // prefix = the threshold key; positions above it are all taken, and the
-    // first `need` positions equal to it
-    int n_eq = 0;
+    // one scan of both counts (each total is at most 32768 < 2^16): this
+    // thread's first output slot is the greater keys before it plus the
+    // equal keys before it that are taken
+    int tot;
+    const int packed = block_excl_scan(n_gt | (n_eq << 16), s_wave, &tot);
+    const int gt_before = packed & 0xffff, eq_before = (int)((unsigned)packed >> 16);
+    const int total = (tot & 0xffff) + min((int)((unsigned)tot >> 16), need);
+    int pos = gt_before + min(eq_before, need);
+    int eq = eq_before;
+    int* o = out + (size_t)qi * topk;
 #pragma unroll
-    for (int j = 0; j < kPer; j++) n_eq += (s0 + j < n && !all && key[j] == prefix) ? 1 : 0;
-    int tmp;
-    const int eq_before = block_excl_scan(n_eq, s_wave, &tmp);
-    int n_sel = 0;
-    {
-        int eq = eq_before;
-#pragma unroll
-        for (int j = 0; j < kPer; j++) {
-            const bool valid = s0 + j < n;
-            bool take = valid && (all || key[j] > prefix);
-            if (valid && !take && key[j] == prefix) take = eq++ < need;
-            n_sel += take ? 1 : 0;
-        }
+    for (int j = 0; j < kPer; j++) {
+        const int s = s0 + j;
+        const bool valid = j < per && s < n;
+        bool take = valid && (all || key[j] > prefix);
+        if (valid && !take && key[j] == prefix) take = eq++ < need;
+        if (take) o[pos++] = s;
     }
-    int total;
-    int pos = block_excl_scan(n_sel, s_wave, &total);
-    {
-        int eq = eq_before;
-        int* o = out + (size_t)qi * topk;
-#pragma unroll
-        for (int j = 0; j < kPer; j++) {
-            const bool valid = s0 + j < n;
-            bool take = valid && (all || key[j] > prefix);
-            if (valid && !take && key[j] == prefix) take = eq++ < need;
-            if (take) o[pos++] = s0 + j;
-        }
-        for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
-    }
+    for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
 }
 
 int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
@@ -265,8 +280,18 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
     }
 #undef AMDMOE_IDX_LAUNCH
     AMDMOE_LAUNCH_CHECK();
-    hipLaunchKernelGGL(indexer_topk_kernel, dim3((unsigned)Q), dim3(kTopkThreads), 0, st, scores,
-                       seq_len, max_seq, topk, out);
+    // registers hold ceil(max_seq / 1024) keys per thread, rounded up to a power of two
+    const int per = (max_seq + kTopkThreads - 1) / kTopkThreads;
+#define AMDMOE_TOPK_LAUNCH(P)                                                                     \
+    hipLaunchKernelGGL(indexer_topk_kernel<P>, dim3((unsigned)Q), dim3(kTopkThreads), 0, st, scores, \
+                       seq_len, max_seq, topk, out)
+    if (per <= 1) AMDMOE_TOPK_LAUNCH(1);
+    else if (per <= 2) AMDMOE_TOPK_LAUNCH(2);
+    else if (per <= 4) AMDMOE_TOPK_LAUNCH(4);
+    else if (per <= 8) AMDMOE_TOPK_LAUNCH(8);
+    else if (per <= 16) AMDMOE_TOPK_LAUNCH(16);
+    else AMDMOE_TOPK_LAUNCH(32);
+#undef AMDMOE_TOPK_LAUNCH
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
