@@ -24,10 +24,12 @@
 //   tid, tid + 1024, ... and each wave counts into its own LDS histogram, so
 //   one atomic instruction covers 64 unrelated positions (a shared
 //   histogram with consecutive positions serialised on the few leading
-//   digits real scores have).  Wave 0 then finds the digit with a suffix
-//   scan across its lanes (4 digits per lane).  The selection takes
-//   ceil(n / 1024) consecutive positions per thread, and one block scan of
-//   the packed (greater, equal) counts places them in ascending order.
+//   digits real scores have; in the first pass the lanes sharing a digit
+//   also combine their counts with a ballot).  Wave 0 then finds the digit
+//   with a suffix scan across its lanes (4 digits per lane).  The selection
+//   keeps the same layout: ballots and per-(wave, slice) counts give each
+//   selected position its slot in ascending order, with no second read of
+//   the row.
 #include "internal.hpp"
 
 namespace amdmoe {
@@ -119,24 +121,9 @@ __device__ __forceinline__ uint32_t score_key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// exclusive block scan of one int per thread (1024 threads)
-__device__ __forceinline__ int block_excl_scan(int v, int* s_wave, int* total) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int x = v;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) s_wave[wave] = x;
-    __syncthreads();
-    int before = 0, all = 0;
-    for (int w = 0; w < kTopkThreads / 64; w++) {
-        if (w < wave) before += s_wave[w];
-        all += s_wave[w];
-    }
-    __syncthreads();
-    *total = all;
-    return before + x - v;
+// number of set bits of m in the lanes below this one
+__device__ __forceinline__ int count_below(unsigned long long m) {
+    return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
 }
 
 template <int kPer>  // positions per thread: max_seq <= 1024 * kPer
@@ -146,7 +133,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
                                                                     int* __restrict__ out) {
     constexpr int kWaves = kTopkThreads / 64;
     __shared__ __align__(16) int s_hist[kWaves][256];  // one histogram per wave
-    __shared__ int s_wave[kWaves];
+    __shared__ unsigned s_slice[kPer + 1];             // counts before each slice, total
     __shared__ int s_sel[2];                           // digit, remaining count
     const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = min(seq_len[qi], max_seq);
@@ -169,9 +156,24 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
         __syncthreads();
         for (int shift = 24; shift >= 0; shift -= 8) {
 #pragma unroll
-            for (int j = 0; j < kPer; j++)
-                if (j * kTopkThreads + tid < n && (key[j] & mask) == prefix)
-                    atomicAdd(&s_hist[wave][(key[j] >> shift) & 0xff], 1);
+            for (int j = 0; j < kPer; j++) {
+                const int d = (key[j] >> shift) & 0xff;
+                bool pending = j * kTopkThreads + tid < n && (key[j] & mask) == prefix;
+                if (shift == 24) {
+                    // leading digits cluster (sign and high exponent bits):
+                    // the lanes sharing the first pending lane's digit add
+                    // with one atomic
+                    const unsigned long long act = __ballot(pending);
+                    if (act != 0) {
+                        const int leader = __ffsll((long long)act) - 1;
+                        const int dl = __builtin_amdgcn_readlane(d, leader);
+                        const unsigned long long m = __ballot(pending && d == dl);
+                        if (lane == leader) atomicAdd(&s_hist[wave][dl], __popcll(m));
+                        pending = pending && d != dl;
+                    }
+                }
+                if (pending) atomicAdd(&s_hist[wave][d], 1);
+            }
             __syncthreads();
             if (wave == 0) {
                 // lane l owns digits 4l..4l+3: their counts over all waves,
@@ -217,38 +219,53 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
         }
     }
     // prefix = the threshold key; positions above it are all taken, and the
-    // first `need` positions equal to it.  Selection in position order:
-    // thread tid takes the `per` consecutive positions from tid * per, their
-    // keys read again (the row is in L2)
-    const int per = (n + kTopkThreads - 1) / kTopkThreads;
-    const int s0 = tid * per;
-    int n_gt = 0, n_eq = 0;
+    // first `need` positions equal to it.  Slice j of the row (positions
+    // j * 1024 + tid) is in position order across the workgroup, so each
+    // position's output slot is the greater / equal keys of the slices
+    // before it, of the waves before it in its slice (LDS counts) and of the
+    // lanes below it (ballots).
+    unsigned* s_cnt = (unsigned*)&s_hist[0][0];  // [wave][slice]: greater | equal << 16
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
-        const int s = s0 + j;
-        key[j] = j < per && s < n ? score_key(row[s]) : 0u;
-        const bool valid = j < per && s < n;
-        n_gt += valid && (all || key[j] > prefix) ? 1 : 0;
-        n_eq += valid && !all && key[j] == prefix ? 1 : 0;
+        const bool valid = j * kTopkThreads + tid < n;
+        const unsigned long long gm = __ballot(valid && (all || key[j] > prefix));
+        const unsigned long long em = __ballot(valid && !all && key[j] == prefix);
+        if (lane == 0) s_cnt[wave * kPer + j] = (unsigned)__popcll(gm) | ((unsigned)__popcll(em) << 16);
     }
-    // one scan of both counts (each total is at most 32768 < 2^16): this
-    // thread's first output slot is the greater keys before it plus the
-    // equal keys before it that are taken
-    int tot;
-    const int packed = block_excl_scan(n_gt | (n_eq << 16), s_wave, &tot);
-    const int gt_before = packed & 0xffff, eq_before = (int)((unsigned)packed >> 16);
-    const int total = (tot & 0xffff) + min((int)((unsigned)tot >> 16), need);
-    int pos = gt_before + min(eq_before, need);
-    int eq = eq_before;
+    __syncthreads();
+    if (wave == 0) {
+        // counts before each (wave, slice) within the slice, in place, then
+        // before each slice (both halves stay below 2^16: n <= 32768)
+        unsigned run = 0;
+        if (lane < kPer)
+            for (int w = 0; w < kWaves; w++) {
+                const unsigned v = s_cnt[w * kPer + lane];
+                s_cnt[w * kPer + lane] = run;
+                run += v;
+            }
+        unsigned x = run;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const unsigned y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane < kPer) s_slice[lane] = x - run;
+        if (lane == kPer - 1) s_slice[kPer] = x;
+    }
+    __syncthreads();
     int* o = out + (size_t)qi * topk;
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
-        const int s = s0 + j;
-        const bool valid = j < per && s < n;
-        bool take = valid && (all || key[j] > prefix);
-        if (valid && !take && key[j] == prefix) take = eq++ < need;
-        if (take) o[pos++] = s;
+        const int s = j * kTopkThreads + tid;
+        const bool valid = s < n;
+        const bool gt = valid && (all || key[j] > prefix), eq = valid && !all && key[j] == prefix;
+        const unsigned long long gm = __ballot(gt), em = __ballot(eq);
+        const unsigned base = s_slice[j] + s_cnt[wave * kPer + j];
+        const int gb = (int)(base & 0xffff) + count_below(gm), eb = (int)(base >> 16) + count_below(em);
+        if (gt || (eq && eb < need)) o[gb + min(eb, need)] = s;
     }
+    const unsigned tot = s_slice[kPer];
+    const int total = (int)(tot & 0xffff) + min((int)(tot >> 16), need);
     for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
 }
 
