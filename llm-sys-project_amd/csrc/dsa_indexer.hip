@@ -8,8 +8,11 @@
 // positions per query by score, ties to the lower position, listed in
 // ascending position order -- the logical indices dsa_decode_bf16_paged takes.
 //
-// indexer_scores_kernel: one workgroup per (query, 256 positions), 4 waves
-//   of 64 positions.  Per 16-position tile one fp8 MFMA per 16 heads,
+// indexer_scores_kernel: a workgroup scores every nparts-th 256-position
+//   tile of one query (the grid is what the device holds at once), 4
+//   waves of 64 positions per tile; a tile's keys are loaded while the one
+//   before it is scored, and its page ids one tile earlier still.  Per
+//   16-position tile one fp8 MFMA per 16 heads,
 //   S (16 positions x 16 heads) = K8 . Q8^T, keys as operand A straight from
 //   the paged cache (two 16-byte loads per lane, a 128-byte row per 4
 //   lanes), the query's heads as operand B held in registers.  Each lane
@@ -30,6 +33,9 @@
 //   keeps the same layout: ballots and per-(wave, slice) counts give each
 //   selected position its slot in ascending order, with no second read of
 //   the row.
+#include <algorithm>
+#include <atomic>
+
 #include "internal.hpp"
 
 namespace amdmoe {
@@ -40,18 +46,106 @@ constexpr int kIdxTile = 256;      // positions per workgroup of the scoring ker
 constexpr int kIdxMaxSeq = 32768;  // positions per query of the selection kernel
 constexpr int kTopkThreads = 1024;
 
-template <int HT>  // head tiles of 16
+// position -> (page, slot): shifts when the page size is a power of two
+template <bool POW2>
+__device__ __forceinline__ int page_of(int s, int page, int shift) { return POW2 ? s >> shift : s / page; }
+template <bool POW2>
+__device__ __forceinline__ int slot_of(int s, int page) { return POW2 ? s & (page - 1) : s % page; }
+
+// sum over the 16 lanes of a row: quad_perm [1,0,3,2], [2,3,0,1], then
+// row_half_mirror and row_mirror (every lane of the row ends with the sum)
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    return dpp_add<0x140>(dpp_add<0x141>(dpp_add<0x4E>(dpp_add<0xB1>(v))));
+}
+
+// the 4 rows of a wave's 16-position tiles for lane r16: page ids of the
+// tile are loaded one step ahead of its keys
+struct IdxRows {
+    int page_id[4];
+};
+
+template <bool POW2>
+__device__ __forceinline__ void idx_load_pages(IdxRows& r, const int* pt, int tb, int wave, int r16, int page,
+                                               int shift, int pages_per_seq) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int s = tb * kIdxTile + 64 * wave + 16 * t + r16;
+        // loaded unconditionally (clamped index) so every wave issues the
+        // same loads and waits can count them; positions past the sequence
+        // are dropped by the key load's s < len (len <= pages_per_seq * page)
+        r.page_id[t] = pt[min(page_of<POW2>(s, page, shift), pages_per_seq - 1)];
+    }
+}
+
+template <bool POW2>
+__device__ __forceinline__ void idx_load_keys(i32x8 (&kf)[4], float (&ksc)[4], const IdxRows& r,
+                                              __amdgpu_buffer_rsrc_t rk, long kc_bytes,
+                                              __amdgpu_buffer_rsrc_t rks, int tb, int wave, int g, int r16,
+                                              int page, int len) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int s = tb * kIdxTile + 64 * wave + 16 * t + r16;
+        const int p = r.page_id[t];
+        long row = (long)p * page + slot_of<POW2>(s, page);
+        if (s >= len || p < 0 || (row + 1) * kIdxD > kc_bytes) row = -1;
+        const uint32_t vo = row >= 0 ? (uint32_t)(row * kIdxD + 16 * g) : kOob;
+        const u32x4 lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0));
+        const u32x4 hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 64, 0));
+        kf[t] = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        ksc[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, row >= 0 ? (uint32_t)(row * 4) : kOob, 0, 0));
+    }
+}
+
+// score one 256-position tile from the wave's keys: lane (g, r16) of the
+// MFMA result holds S[4g + i][r16], positions 4g + i of a 16-tile, head r16
+template <int HT>
+__device__ __forceinline__ void idx_score_tile(const i32x8 (&kf)[4], const float (&ksc)[4], const i32x8 (&qf)[HT],
+                                               const float (&wq)[HT], int tb, int wave, int g, int r16, int len,
+                                               int max_seq, float* __restrict__ srow) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < HT; h++) {
+            const f32x4 c = mfma_fp8(kf[t], qf[h], (f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] += wq[h] * fmaxf(c[i], 0.0f);
+        }
+        // sum over the 16 heads of each head tile: across the 16 lanes of a row
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = row16_sum(v[i]);
+        // lane (g, n < 4) writes position 4g + n with the scale of its row,
+        // held by the lane that loaded that row (r16 = 4g + n)
+        const int n = r16 & 3;
+        const float sc = __shfl(ksc[t], 4 * g + n, 64);
+        const float tot = n == 0 ? v[0] : (n == 1 ? v[1] : (n == 2 ? v[2] : v[3]));
+        const int s = tb * kIdxTile + 64 * wave + 16 * t + 4 * g + n;
+        if (r16 < 4 && s < max_seq) srow[s] = s < len ? tot * sc : -INFINITY;
+    }
+}
+
+template <int HT, bool POW2>  // head tiles of 16; page size a power of two (2^shift)
 __global__ __launch_bounds__(256) void indexer_scores_kernel(
     const uint8_t* __restrict__ qc, const float* __restrict__ qs, const float* __restrict__ hw,
     const uint8_t* __restrict__ kc, long kc_bytes, const float* __restrict__ ks,
-    const int* __restrict__ page_table, const int* __restrict__ seq_len, int Q, int page,
-    int pages_per_seq, int max_seq, int ntile, float* __restrict__ scores) {
-    const int qi = blockIdx.x / ntile, tb = blockIdx.x - qi * ntile;
+    const int* __restrict__ page_table, const int* __restrict__ seq_len, int Q, int page, int shift,
+    int pages_per_seq, int max_seq, int ntile, int nparts, float* __restrict__ scores) {
+    const int qi = blockIdx.x / nparts, part = blockIdx.x - qi * nparts;
     if (qi >= Q) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, r16 = lane & 15;
-    const int len = min(seq_len[qi], max_seq);
-    const long seq = (long)pages_per_seq * page;
+    const int* pt = page_table + (size_t)qi * pages_per_seq;
+    // page ids of the first two tiles go out before anything else
+    IdxRows pa, pb;
+    idx_load_pages<POW2>(pa, pt, part, wave, r16, page, shift, pages_per_seq);
+    idx_load_pages<POW2>(pb, pt, part + nparts, wave, r16, page, shift, pages_per_seq);
+    // positions at or past seq_len and past the cache's capacity score -inf
+    const int len = min(min(seq_len[qi], max_seq), pages_per_seq * page);
     constexpr int Hi = 16 * HT;
 
     // the query's heads as B operands: head 16h + r16, bytes 16g.. and 64+16g..
@@ -67,50 +161,28 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(
         wq[h] = hw[hq] * qs[hq];
     }
 
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc, kc_bytes);
-    const int* pt = page_table + (size_t)qi * pages_per_seq;
-    // this wave's 4 tiles of 16 positions: keys (operand A) and scales
-    constexpr int kTiles = 4;
-    i32x8 kf[kTiles];
-    float ksc[kTiles];
-#pragma unroll
-    for (int t = 0; t < kTiles; t++) {
-        const int s = tb * kIdxTile + 64 * wave + 16 * t + r16;
-        long row = -1;
-        if (s < len) {
-            const int p = pt[s / page];
-            row = (long)p * page + s % page;
-            if (p < 0 || row < 0 || (long)s >= seq) row = -1;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc, kc_bytes), rks = make_rsrc(ks, kc_bytes / kIdxD * 4);
+    float* srow = scores + (size_t)qi * max_seq;
+    // two key buffers in turn (A for tiles part, part + 2 nparts, ...; B for
+    // the ones between): a tile's keys are loaded while the one before it
+    // is scored, and its page ids one tile earlier still.  Page ids go out
+    // before keys, as loads complete in issue order.
+    i32x8 ka[4], kb[4];
+    float sa[4], sb[4];
+    idx_load_keys<POW2>(ka, sa, pa, rk, kc_bytes, rks, part, wave, g, r16, page, len);
+    for (int tb = part; tb < ntile; tb += 2 * nparts) {
+        const int t1 = tb + nparts, t2 = t1 + nparts;
+        if (t1 < ntile) {
+            idx_load_pages<POW2>(pa, pt, t2, wave, r16, page, shift, pages_per_seq);
+            idx_load_keys<POW2>(kb, sb, pb, rk, kc_bytes, rks, t1, wave, g, r16, page, len);
         }
-        const uint32_t vo = row >= 0 && (row + 1) * kIdxD <= kc_bytes ? (uint32_t)(row * kIdxD + 16 * g) : kOob;
-        const u32x4 lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, 0));
-        const u32x4 hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 64, 0));
-        kf[t] = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        ksc[t] = row >= 0 ? ks[row] : 0.0f;
-    }
-#pragma unroll
-    for (int t = 0; t < kTiles; t++) {
-        // lane (g, r16) holds S[4g + i][r16]: positions 4g + i of the tile, head r16
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int h = 0; h < HT; h++) {
-            const f32x4 c = mfma_fp8(kf[t], qf[h], (f32x4){0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[i] += wq[h] * fmaxf(c[i], 0.0f);
+        idx_score_tile<HT>(ka, sa, qf, wq, tb, wave, g, r16, len, max_seq, srow);
+        if (t1 >= ntile) break;
+        if (t2 < ntile) {
+            idx_load_pages<POW2>(pb, pt, t2 + nparts, wave, r16, page, shift, pages_per_seq);
+            idx_load_keys<POW2>(ka, sa, pa, rk, kc_bytes, rks, t2, wave, g, r16, page, len);
         }
-        // sum over the 16 heads of each head tile: butterfly within 16 lanes
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1)
-#pragma unroll
-            for (int i = 0; i < 4; i++) v[i] += __shfl_xor(v[i], o, 16);
-        // lane (g, n < 4) writes position 4g + n with the scale of its row,
-        // held by the lane that loaded that row (r16 = 4g + n)
-        const int n = r16 & 3;
-        const float sc = __shfl(ksc[t], 4 * g + n, 64);
-        const float tot = n == 0 ? v[0] : (n == 1 ? v[1] : (n == 2 ? v[2] : v[3]));
-        const int s = tb * kIdxTile + 64 * wave + 16 * t + 4 * g + n;
-        if (r16 < 4 && s < max_seq) scores[(size_t)qi * max_seq + s] = s < len ? tot * sc : -INFINITY;
+        idx_score_tile<HT>(kb, sb, qf, wq, t1, wave, g, r16, len, max_seq, srow);
     }
 }
 
@@ -269,6 +341,32 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
 }
 
+// compute units of the current device (256 on MI355X), looked up once per device
+static int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// resident workgroups of the scoring kernel per CU (its register use sets it)
+template <int HT, bool P2>
+static int scores_blocks_per_cu() {
+    static std::atomic<int> cache{0};
+    int b = cache.load(std::memory_order_relaxed);
+    if (b <= 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, indexer_scores_kernel<HT, P2>, 256, 0) != hipSuccess || b <= 0)
+            b = 1;
+        cache.store(b, std::memory_order_relaxed);
+    }
+    return b;
+}
+
 int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
                        long kc_rows, const float* ks, const int* page_table, const int* seq_len,
                        int Q, int Hi, int page, int pages_per_seq, int max_seq, int topk,
@@ -282,12 +380,25 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
     AMDMOE_CHECK_ARG(kc_rows * kIdxD < 0x7FFFFFF0L, "dsa_indexer: key cache of %ld rows exceeds 2 GiB", kc_rows);
     if (Q == 0) return AMDMOE_OK;
     const int ntile = (max_seq + kIdxTile - 1) / kIdxTile;
-    const long grid = (long)Q * ntile;
-    AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_indexer: grid too large");
+    AMDMOE_CHECK_ARG((long)Q * ntile < (1L << 31), "dsa_indexer: grid too large");
     const long kb = kc_rows * kIdxD;
-#define AMDMOE_IDX_LAUNCH(HT)                                                                        \
-    hipLaunchKernelGGL(indexer_scores_kernel<HT>, dim3((unsigned)grid), dim3(256), 0, st, qc, qs, hw, \
-                       kc, kb, ks, page_table, seq_len, Q, page, pages_per_seq, max_seq, ntile, scores)
+    // each workgroup scores tiles part, part + nparts, ... of one query, the
+    // grid sized to the workgroups the device holds at once
+#define AMDMOE_IDX_LAUNCH2(HT, P2)                                                                      \
+    do {                                                                                               \
+        const long target = (long)scores_blocks_per_cu<HT, P2>() * device_cu_count();                 \
+        const int nparts = (int)std::max(1L, std::min((long)ntile, (target + Q - 1) / Q));             \
+        hipLaunchKernelGGL((indexer_scores_kernel<HT, P2>), dim3((unsigned)((long)Q * nparts)), dim3(256), \
+                           0, st, qc, qs, hw, kc, kb, ks, page_table, seq_len, Q, page, shift,          \
+                           pages_per_seq, max_seq, ntile, nparts, scores);                             \
+    } while (0)
+#define AMDMOE_IDX_LAUNCH(HT)                  \
+    do {                                       \
+        if (pow2) AMDMOE_IDX_LAUNCH2(HT, true);  \
+        else AMDMOE_IDX_LAUNCH2(HT, false);      \
+    } while (0)
+    const bool pow2 = (page & (page - 1)) == 0;
+    const int shift = pow2 ? __builtin_ctz((unsigned)page) : 0;
     switch (Hi / 16) {
         case 1: AMDMOE_IDX_LAUNCH(1); break;
         case 2: AMDMOE_IDX_LAUNCH(2); break;
@@ -296,6 +407,7 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
         default: return set_error(AMDMOE_ERR_INVALID, "dsa_indexer: Hi=%d must be 16, 32, 64 or 128", Hi);
     }
 #undef AMDMOE_IDX_LAUNCH
+#undef AMDMOE_IDX_LAUNCH2
     AMDMOE_LAUNCH_CHECK();
     // registers hold ceil(max_seq / 1024) keys per thread, rounded up to a power of two
     const int per = (max_seq + kTopkThreads - 1) / kTopkThreads;

@@ -82,7 +82,8 @@ def test_oracle_topk_tie_rule(orc):
 @pytest.mark.gpu
 @pytest.mark.parametrize("Q,Hi,ctx,page,topk", [(3, 64, 4096, 64, 512), (2, 16, 1024, 16, 100),
                                                 (2, 128, 2048, 64, 2048), (4, 32, 640, 32, 64),
-                                                (2, 32, 8192, 64, 2048), (2, 16, 16384, 64, 1000)])
+                                                (2, 32, 8192, 64, 2048), (2, 16, 16384, 64, 1000),
+                                                (2, 16, 960, 48, 100)])
 def test_gpu_indexer_bit_exact_on_exact_scores(amd, orc, Q, Hi, ctx, page, topk):
     import torch
     print(f"indexer exact Q={Q} Hi={Hi} ctx={ctx} topk={topk}", flush=True)
