@@ -401,6 +401,70 @@ __global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
     }
 }
 
+// perm_small_kernel: decode-sized batches (T*K <= 1024 slots, E <= 256) in
+// one workgroup and one launch.  Thread i owns slot i = t*K + k; wave w sets
+// bit `lane` of its own 64-bit mask for the slot's expert, so a slot's row
+// is its expert's offset + the slots of that expert in earlier waves + in
+// lower lanes of its wave: flat slot order = ascending token order, as in
+// the multi-block path.
+constexpr int kSmallSlots = 1024;
+constexpr int kSmallMaxE = 256;
+
+__global__ __launch_bounds__(kSmallSlots) void perm_small_kernel(
+    const int* __restrict__ idx, int T, int K, int E, int BM, int* __restrict__ counts,
+    int* __restrict__ offsets, int4* __restrict__ tiles, int* __restrict__ num_tiles,
+    int* __restrict__ sorted_token, int* __restrict__ sorted_slot, const float* __restrict__ wts,
+    float* __restrict__ sorted_w) {
+    constexpr int kWaves = kSmallSlots / 64;
+    __shared__ unsigned long long s_mask[kWaves][kSmallMaxE];
+    __shared__ int s_off[kSmallMaxE];
+    __shared__ int s_wr[kWaves], s_wt[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < kWaves * kSmallMaxE; i += kSmallSlots) (&s_mask[0][0])[i] = 0ull;
+    __syncthreads();
+    const int e = tid < T * K ? slot_expert(idx, tid, K, E) : -1;
+    if (e >= 0) atomicOr(&s_mask[wave][e], 1ull << lane);
+    __syncthreads();
+    // thread e < E: the expert's rows and M-tiles, exclusive scans over experts
+    int tot = 0, tl = 0;
+    if (tid < E) {
+        for (int w = 0; w < kWaves; w++) tot += __popcll(s_mask[w][tid]);
+        tl = (tot + BM - 1) / BM;
+    }
+    int rs = tot, ts = tl;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ro = __shfl_up(rs, o, 64), to = __shfl_up(ts, o, 64);
+        if (lane >= o) { rs += ro; ts += to; }
+    }
+    if (lane == 63) { s_wr[wave] = rs; s_wt[wave] = ts; }
+    __syncthreads();
+    int wr = 0, wt = 0, ar = 0, at = 0;
+    for (int w = 0; w < kWaves; w++) {
+        if (w < wave) { wr += s_wr[w]; wt += s_wt[w]; }
+        ar += s_wr[w];
+        at += s_wt[w];
+    }
+    if (tid < E) {
+        const int row_off = wr + rs - tot, tile_off = wt + ts - tl;
+        s_off[tid] = row_off;
+        counts[tid] = tot;
+        offsets[tid] = row_off;
+        for (int j = 0; j < tl; j++) tiles[tile_off + j] = mtile(tid, row_off, tot, BM, j);
+    }
+    if (tid == 0) {
+        offsets[E] = ar;
+        *num_tiles = at;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        int pos = s_off[e] + __popcll(s_mask[wave][e] & ((1ull << lane) - 1ull));
+        for (int w = 0; w < wave; w++) pos += __popcll(s_mask[w][e]);
+        sorted_token[pos] = tid / K;
+        sorted_slot[pos] = tid;
+        if (sorted_w) sorted_w[pos] = wts[tid];
+    }
+}
+
 size_t permute_scratch_bytes(int T, int E) {
     const long nblk = (T + kPermTok - 1) / kPermTok;
     if (E > 1024 || nblk * E > (1L << 22)) return 0;
@@ -411,6 +475,12 @@ int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
                    int* scratch, const float* wts, float* sorted_w, hipStream_t st) {
     AMDMOE_CHECK_ARG((wts == nullptr) == (sorted_w == nullptr), "permute: wts and sorted_w go together");
+    if (T > 0 && (long)T * K <= kSmallSlots && E <= kSmallMaxE) {
+        hipLaunchKernelGGL(perm_small_kernel, dim3(1), dim3(kSmallSlots), 0, st, idx, T, K, E, BM, counts,
+                           offsets, tiles, num_tiles, sorted_token, sorted_slot, wts, sorted_w);
+        AMDMOE_LAUNCH_CHECK();
+        return AMDMOE_OK;
+    }
     if (scratch && T > 0 && permute_scratch_bytes(T, E) > 0) {
         const int nblk = (T + kPermTok - 1) / kPermTok;
         int* blk_cnt = scratch;
