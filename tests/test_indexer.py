@@ -103,6 +103,28 @@ def test_gpu_indexer_bit_exact_on_exact_scores(amd, orc, Q, Hi, ctx, page, topk)
 
 
 @pytest.mark.gpu
+def test_gpu_indexer_empty_and_overlong_sequences(amd, orc):
+    """seq_len 0 (every score -inf, every index -1), seq_len past max_seq
+    (clamped to max_seq) and seq_len 1, bit-exact against the oracle."""
+    import torch
+    Q, Hi, ctx, page, topk = 3, 16, 512, 64, 100
+    print(f"indexer edge lengths Q={Q} ctx={ctx} topk={topk}", flush=True)
+    qc, qs, hw, kc, ks, pt = exact_inputs(Q, Hi, ctx, page, 7)
+    sl = np.array([0, ctx + 188, 1], np.int32)
+    ref_sc = orc.dsa_indexer_scores(qc, qs, hw, kc, ks, pt, sl, page, ctx)
+    ref_ix = orc.dsa_indexer_topk(ref_sc, sl, topk)
+    assert (ref_ix[0] == -1).all() and ref_ix[2, 0] == 0 and (ref_ix[2, 1:] == -1).all()
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    scores = torch.empty((Q, ctx), dtype=torch.float32, device="cuda")
+    out = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    amd.dsa_indexer_topk_fp8(d(qc), d(qs), d(hw), d(kc), d(ks), d(pt), d(sl), page, ctx, topk,
+                             scores, out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(scores.cpu().numpy(), ref_sc)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref_ix)
+
+
+@pytest.mark.gpu
 def test_gpu_indexer_random_baseline_shape(amd, orc):
     """BASELINE decode shape on 4 queries: 64 index heads, 32768 positions,
     top-2048, random fp8 data."""
