@@ -137,10 +137,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
         base += total;
     }
 
-    for (int j = tid; j * BM < cnt; j += kPermThreads) {
-        int r0 = j * BM;
-        tiles[tile_off + j] = mtile(e, row_off, cnt, BM, j);
-    }
+    for (int j = tid; j * BM < cnt; j += kPermThreads) tiles[tile_off + j] = mtile(e, row_off, cnt, BM, j);
     if (tid == 0) {
         counts[e] = cnt;
         offsets[e] = row_off;

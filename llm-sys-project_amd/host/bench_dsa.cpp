@@ -24,7 +24,7 @@
     } while (0)
 
 static void random_fill(float* data, size_t n, float lo, float hi) {
-    for (size_t i = 0; i < n; i++) data[i] = lo + static_cast<float>(rand()) / RAND_MAX * (hi - lo);
+    for (size_t i = 0; i < n; i++) data[i] = lo + static_cast<float>(rand()) / static_cast<float>(RAND_MAX) * (hi - lo);
 }
 
 // tests/test_dsa.cu:73-85 (partial Fisher-Yates, then sorted)

@@ -26,7 +26,7 @@
 
 // utils/cuda_utils.cuh:56-60
 static void random_fill(float* data, size_t n, float lo, float hi) {
-    for (size_t i = 0; i < n; i++) data[i] = lo + static_cast<float>(rand()) / RAND_MAX * (hi - lo);
+    for (size_t i = 0; i < n; i++) data[i] = lo + static_cast<float>(rand()) / static_cast<float>(RAND_MAX) * (hi - lo);
 }
 
 static float* upload(const std::vector<float>& h) {
