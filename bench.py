@@ -273,7 +273,8 @@ def pmc_averages(csv_dir):
                     dispatches=max(len(v) for v in cs.values())) for k, cs in agg.items()}
 
 
-def traffic_summary(fetch_dir, write_dir, out_md, out_json, command):
+def traffic_summary(fetch_dir, write_dir, out_md, out_json, command,
+                    title="HBM traffic per launch: DSV3 fp8 MoE layer, T=4096 (+ DSA decode)"):
     """HBM bytes per launch from a FETCH_SIZE run and a WRITE_SIZE run of the
     same command with --calibrate-copy: the 1 GiB device-to-device copy
     (rocclr copyBuffer dispatches, 1 GiB read + 1 GiB written in all) gives
@@ -296,7 +297,7 @@ def traffic_summary(fetch_dir, write_dir, out_md, out_json, command):
                       "bytes": fb + wb}
         rows.append(f"| `{k}` | {fa[k]['FETCH_SIZE']:.4g} | {wa[k]['WRITE_SIZE']:.4g} | "
                     f"{(fb + wb) / 1e9:.3f} GB |")
-    lines = ["# HBM traffic per launch: DSV3 fp8 MoE layer, T=4096 (+ DSA decode)", "",
+    lines = [f"# {title}", "",
              "Two counter runs and the summary (from the repository root on the GPU box):", "",
              "```", command, "```", "",
              f"Calibration: `--calibrate-copy` runs one 1 GiB device-to-device copy first "
@@ -394,8 +395,8 @@ def main():
         stats_summary(*sys.argv[2:6])
         return
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic-summary":
-        # bench.py --traffic-summary FETCH_DIR WRITE_DIR OUT_MD OUT_JSON COMMAND
-        traffic_summary(*sys.argv[2:7])
+        # bench.py --traffic-summary FETCH_DIR WRITE_DIR OUT_MD OUT_JSON COMMAND [TITLE]
+        traffic_summary(*sys.argv[2:8])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--sweep", metavar="JSON",

@@ -17,6 +17,15 @@
  *     workspace, grown on demand (that first call allocates).  A non-NULL
  *     workspace must hold amdmoe_moe_workspace_bytes() bytes; calls that
  *     share one workspace must be ordered on one stream.
+ *   - Entry points without a workspace argument that need scratch (the
+ *     split-K routing of amdmoe_moe_gate_bf16/_fp8, amdmoe_moe_permute,
+ *     amdmoe_dsa_decode_bf16_paged, amdmoe_dsa_forward_f32 with S > 16384)
+ *     use a per-device buffer of their own family (routing, permutation,
+ *     decode, fp32 DSA; none is shared with the MoE forward's workspace or
+ *     with another family).  A call that must grow that buffer frees and
+ *     allocates it, which waits for the device; calls of one family that use
+ *     the buffer must be ordered on one stream (concurrent calls of one
+ *     family on two streams race on it).
  *   - bf16 tensors are passed as uint16_t (bfloat16 bit patterns), fp8 as
  *     uint8_t OCP e4m3 ("E4M3FN") codes.
  */
@@ -74,10 +83,21 @@ int amdmoe_moe_workspace_bytes(const MoeConfig* cfg, int dtype, size_t* bytes);
 
 /* Full MoE layer, fp32.  Replaces moe_forward (kernels/moe/naive_moe.cuh:74-76,
  * kernels/moe/naive_moe.cu:400-471): x [T,D], Wg [E,D], W1 [E,2I,D] (gate rows
- * 0..I-1, up rows I..2I-1), W2 [E,D,I]; y [T,D] is overwritten. */
+ * 0..I-1, up rows I..2I-1), W2 [E,D,I]; y [T,D] is overwritten.  Any D and I
+ * (D and I multiples of 32 run on MFMA, other shapes on bounds-checked fp32
+ * kernels). */
 int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float* w1,
                            const float* w2, float* y, const MoeConfig* cfg,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* The fp32 layer with a per-expert logit bias (BASELINE medium-fp32 config,
+ * whose skewed expert loads come from the bias).  No counterpart in the
+ * reference (moe_forward has no bias, naive_moe.cuh:74-76); same arguments
+ * and result as amdmoe_moe_forward_f32, with gate_bias fp32 [E] added to
+ * each token's logits before the softmax (NULL = no bias). */
+int amdmoe_moe_forward_f32_bias(const float* x, const float* gate_weight, const float* gate_bias,
+                                const float* w1, const float* w2, float* y, const MoeConfig* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Full MoE layer, bf16 storage with fp32 accumulation (BASELINE medium-bf16
  * and Mixtral configs; same layouts as moe_forward).  gate_weight is fp32,
@@ -210,7 +230,11 @@ int amdmoe_set_stage_events(void** events);
 
 /* Sparse MLA decode, fp32: replaces dsa_forward (naive_dsa.cuh:81-87,
  * naive_dsa.cu:435-474).  q_nope [Q,H,Dc], q_pe [Q,H,Dp], kv_c [N,Dc],
- * kv_p [N,Dp], v [N,Dc], sparse_indices [Q,S] (flat rows); out [Q,H,Dc]. */
+ * kv_p [N,Dp], v [N,Dc], sparse_indices [Q,S] (flat rows); out [Q,H,Dc].
+ * Any S (S > 16384 keeps the scores in the entry's cached scratch).  An
+ * index outside [0, N) (N = cfg->total_kv_tokens) selects nothing: it takes
+ * no part in the softmax and no row is read for it; a query with no valid
+ * index gets 0 (the reference reads such an index out of bounds). */
 int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* kv_cache_compressed,
                            const float* kv_cache_positional, const float* v_cache,
                            const int* sparse_indices, float* output, const DsaConfig* cfg,
@@ -222,8 +246,14 @@ int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* 
  * [Q, pages_per_seq]; logical_indices int32 [Q,S] are positions in the
  * query's sequence, physical row = page_table[q][i/page]*page + i%page.
  * q_nope bf16 [Q,H,Dc], q_pe bf16 [Q,H,Dp]; out bf16 [Q,H,Dc].
- * cfg->total_kv_tokens is the number of rows of `cache` (it bounds every
- * access); cfg->page_size is the page length.
+ * cfg->total_kv_tokens is the number of rows of `cache`; cfg->page_size is
+ * the page length.  A selected position selects nothing when it lies
+ * outside [0, pages_per_seq * page), when its page-table entry is negative
+ * or when its row is at or past total_kv_tokens: no page-table entry or
+ * cache row is read for it and it takes no part in the softmax, so the
+ * output is attention over the valid positions only (0 for a query with
+ * none).  The -1 padding of amdmoe_dsa_indexer_topk_fp8 (sequences shorter
+ * than the selection) is therefore decoded correctly.
  * Requires Dc == 512, Dp == 64, H a multiple of 32, 1 <= S <= 4096. */
 int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const uint16_t* cache, const int* page_table,

@@ -17,7 +17,7 @@ AMDMOE_DTYPE_FP8 = 2
 # Exported symbols, in the order include/amdmoe.h declares them.
 SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
-    "amdmoe_moe_forward_f32", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
+    "amdmoe_moe_forward_f32", "amdmoe_moe_forward_f32_bias", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
     "amdmoe_moe_forward_fp8_packed", "amdmoe_pack_weights_fp8",
     "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16", "amdmoe_moe_gate_fp8",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
@@ -69,6 +69,7 @@ def load():
         "amdmoe_version": (ctypes.c_char_p, []),
         "amdmoe_moe_workspace_bytes": (I, [cfgp, I, ctypes.POINTER(SZ)]),
         "amdmoe_moe_forward_f32": (I, [_P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_moe_forward_f32_bias": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_bf16": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8_packed": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
@@ -150,6 +151,13 @@ def moe_forward_f32(x, wg, w1, w2, y, cfg, ws=None, stream=None):
     p, n = _ws(ws)
     _check(load().amdmoe_moe_forward_f32(_ptr(x), _ptr(wg), _ptr(w1), _ptr(w2), _ptr(y),
                                          ctypes.byref(cfg), p, n, _stream(stream)))
+
+
+def moe_forward_f32_bias(x, wg, bias, w1, w2, y, cfg, ws=None, stream=None):
+    """amdmoe_moe_forward_f32 with a per-expert logit bias [E] (None: no bias)."""
+    p, n = _ws(ws)
+    _check(load().amdmoe_moe_forward_f32_bias(_ptr(x), _ptr(wg), _ptr(bias), _ptr(w1), _ptr(w2),
+                                              _ptr(y), ctypes.byref(cfg), p, n, _stream(stream)))
 
 
 def moe_forward_bf16(x, wg, bias, w1, w2, y, cfg, ws=None, stream=None):

@@ -94,19 +94,25 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     return w;
 }
 
-// Per-device cached workspace for calls that pass workspace == NULL.
+// Per-device cached scratch for calls that take no workspace (or pass
+// workspace == NULL), one buffer per entry-point family, so that calls of
+// different families (an MoE forward on one stream, a decode on another)
+// never share memory.  Calls of one family that use it must be ordered on
+// one stream; the call that grows a buffer frees and allocates (hipFree
+// waits for the device).
+enum ScratchKind { SCR_MOE = 0, SCR_GATE, SCR_PERMUTE, SCR_DSA_DECODE, SCR_DSA_F32, SCR_KINDS };
 struct CachedWs {
     std::mutex m;
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-static CachedWs g_cache[64];
+static CachedWs g_cache[64][SCR_KINDS];
 
-static int cached_workspace(size_t need, void** out) {
+static int cached_workspace(size_t need, void** out, int kind = SCR_MOE) {
     int dev = 0;
     AMDMOE_HIP_TRY(hipGetDevice(&dev));
     AMDMOE_CHECK_ARG(dev >= 0 && dev < 64, "device id %d out of range", dev);
-    CachedWs& c = g_cache[dev];
+    CachedWs& c = g_cache[dev][kind];
     std::lock_guard<std::mutex> lk(c.m);
     if (c.bytes < need) {
         if (c.ptr) AMDMOE_HIP_TRY(hipFree(c.ptr));  // hipFree waits for pending work
@@ -129,11 +135,27 @@ static int check_cfg(const MoeConfig* cfg, int dtype) {
     AMDMOE_CHECK_ARG(c.top_k >= 1 && c.top_k <= 64, "top_k=%d outside [1, 64]", c.top_k);
     AMDMOE_CHECK_ARG(c.hidden_dim >= 1 && c.intermediate_dim >= 1, "hidden_dim=%d / intermediate_dim=%d must be positive", c.hidden_dim, c.intermediate_dim);
     AMDMOE_CHECK_ARG((long)c.num_tokens * c.top_k < (1L << 30), "T*K=%ld too large", (long)c.num_tokens * c.top_k);
-    const int kq = dtype == AMDMOE_DTYPE_F32 ? 32 : (dtype == AMDMOE_DTYPE_BF16 ? 64 : 128);
+    // fp32 (the reference's format) takes any D and I; the bf16 / fp8 tiles
+    // need whole 64- / 128-element K steps (and the fp8 block scales 128)
+    const int kq = dtype == AMDMOE_DTYPE_F32 ? 1 : (dtype == AMDMOE_DTYPE_BF16 ? 64 : 128);
     AMDMOE_CHECK_ARG(c.hidden_dim % kq == 0 && c.intermediate_dim % kq == 0,
                      "hidden_dim=%d and intermediate_dim=%d must be multiples of %d for this dtype",
                      c.hidden_dim, c.intermediate_dim, kq);
     return AMDMOE_OK;
+}
+
+// Routing entries: any D (the gate GEMM is not tiled along D there), I unused.
+static int check_gate_cfg(const MoeConfig* cfg) {
+    AMDMOE_CHECK_ARG(cfg != nullptr, "cfg is NULL");
+    MoeConfig c = *cfg;
+    c.intermediate_dim = 1;
+    return check_cfg(&c, AMDMOE_DTYPE_F32);
+}
+
+// fp32 D and I the MFMA kernels tile (whole 32-element K steps); other
+// shapes take the bounds-checked kernels of moe_generic.hip
+static bool f32_mfma_shape(const MoeConfig& c) {
+    return c.hidden_dim % 32 == 0 && c.intermediate_dim % 32 == 0;
 }
 
 static int resolve_ws(const MoeConfig& c, int dtype, void* workspace, size_t bytes, MoeWs* out) {
@@ -171,6 +193,15 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
                        w.sorted_slot, w.tiles, w.num_tiles,
                        permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st));
     TRY(mark(3, st));
+    if (dt == DT_F32 && !f32_mfma_shape(c)) {
+        TRY(launch_experts_f32_any((const float*)a_x, (const float*)w1, (const float*)w2, T, E, K,
+                                   D, I, w.tiles, w.num_tiles, mtiles, w.sorted_token,
+                                   w.sorted_slot, w.sorted_w, w.idx, (float*)w.act,
+                                   (float*)w.ypair, (float*)y, st));
+        TRY(mark(4, st));
+        TRY(mark(5, st));
+        return mark(6, st);
+    }
     GemmArgs up{};
     up.a = a_x;
     up.a_bytes = (long)T * D * es;
@@ -242,9 +273,9 @@ int amdmoe_moe_workspace_bytes(const MoeConfig* cfg, int dtype, size_t* bytes) {
     return AMDMOE_OK;
 }
 
-int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float* w1,
-                           const float* w2, float* y, const MoeConfig* cfg, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+static int forward_f32(const float* x, const float* gate_weight, const float* gate_bias,
+                       const float* w1, const float* w2, float* y, const MoeConfig* cfg,
+                       void* workspace, size_t workspace_bytes, void* stream) {
     TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
     const MoeConfig& c = *cfg;
     if (c.num_tokens == 0) return AMDMOE_OK;
@@ -253,12 +284,25 @@ int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float
     MoeWs w;
     TRY(resolve_ws(c, AMDMOE_DTYPE_F32, workspace, workspace_bytes, &w));
     TRY(mark(0, st));
-    TRY(launch_route_exact<float, float>(x, gate_weight, nullptr, c.num_tokens, c.num_experts,
+    TRY(launch_route_exact<float, float>(x, gate_weight, gate_bias, c.num_tokens, c.num_experts,
                                          c.top_k, c.hidden_dim, w.idx, w.wts, st));
     TRY(mark(1, st));
     TRY(mark(2, st));
     return moe_experts(DT_F32, c, w, (const uint8_t*)x, nullptr, (const uint8_t*)w1, nullptr,
                        (const uint8_t*)w2, nullptr, y, st);
+}
+
+int amdmoe_moe_forward_f32(const float* x, const float* gate_weight, const float* w1,
+                           const float* w2, float* y, const MoeConfig* cfg, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    return forward_f32(x, gate_weight, nullptr, w1, w2, y, cfg, workspace, workspace_bytes, stream);
+}
+
+int amdmoe_moe_forward_f32_bias(const float* x, const float* gate_weight, const float* gate_bias,
+                                const float* w1, const float* w2, float* y, const MoeConfig* cfg,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+    return forward_f32(x, gate_weight, gate_bias, w1, w2, y, cfg, workspace, workspace_bytes,
+                       stream);
 }
 
 int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
@@ -336,7 +380,7 @@ int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int col
 
 int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_indices,
                         float* expert_weights, const MoeConfig* cfg, void* stream) {
-    TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
+    TRY(check_gate_cfg(cfg));
     if (cfg->num_tokens == 0) return AMDMOE_OK;
     return launch_route_exact<float, float>(x, gate_weight, nullptr, cfg->num_tokens,
                                             cfg->num_experts, cfg->top_k, cfg->hidden_dim,
@@ -346,7 +390,7 @@ int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_in
 int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const float* gate_bias,
                           int* expert_indices, float* expert_weights, const MoeConfig* cfg,
                           void* stream) {
-    TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
+    TRY(check_gate_cfg(cfg));
     if (cfg->num_tokens == 0) return AMDMOE_OK;
     return launch_route_exact<uint16_t, float>(x, gate_weight, gate_bias, cfg->num_tokens,
                                                cfg->num_experts, cfg->top_k, cfg->hidden_dim,
@@ -356,14 +400,14 @@ int amdmoe_moe_gate_bf16x(const uint16_t* x, const float* gate_weight, const flo
 
 int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
                          float* expert_weights, const MoeConfig* cfg, void* stream) {
-    TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
+    TRY(check_gate_cfg(cfg));
     if (cfg->num_tokens == 0) return AMDMOE_OK;
     if (route_mfma_supported(cfg->num_experts, cfg->top_k, cfg->hidden_dim)) {
         // logits scratch: the library's cached per-device workspace
         void* scratch = nullptr;
         TRY(cached_workspace(route_mfma_scratch_bytes(cfg->num_tokens, cfg->num_experts,
                                                       cfg->hidden_dim, false),
-                             &scratch));
+                             &scratch, SCR_GATE));
         return launch_route_mfma(x, gate_weight, cfg->num_tokens, cfg->num_experts, cfg->top_k,
                                  cfg->hidden_dim, expert_indices, expert_weights, (float*)scratch,
                                  nullptr, nullptr, (hipStream_t)stream);
@@ -377,7 +421,9 @@ int amdmoe_moe_gate_bf16(const uint16_t* x, const uint16_t* gate_weight, int* ex
 int amdmoe_moe_gate_fp8(const uint16_t* x, const uint16_t* gate_weight, int* expert_indices,
                         float* expert_weights, uint8_t* xq, float* x_scale, const MoeConfig* cfg,
                         void* stream) {
-    TRY(check_cfg(cfg, AMDMOE_DTYPE_FP8));
+    TRY(check_gate_cfg(cfg));
+    AMDMOE_CHECK_ARG(cfg->hidden_dim % 128 == 0, "moe_gate_fp8: hidden_dim=%d not a multiple of 128",
+                     cfg->hidden_dim);
     AMDMOE_CHECK_ARG(x && gate_weight && expert_indices && expert_weights && xq && x_scale,
                      "null tensor pointer");
     const MoeConfig& c = *cfg;
@@ -386,7 +432,7 @@ int amdmoe_moe_gate_fp8(const uint16_t* x, const uint16_t* gate_weight, int* exp
     if (route_mfma_supported(c.num_experts, c.top_k, c.hidden_dim)) {
         void* scratch = nullptr;
         TRY(cached_workspace(route_mfma_scratch_bytes(c.num_tokens, c.num_experts, c.hidden_dim, true),
-                             &scratch));
+                             &scratch, SCR_GATE));
         return launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
                                  expert_indices, expert_weights, (float*)scratch, xq, x_scale, st);
     }
@@ -400,7 +446,7 @@ int amdmoe_moe_gather_f32(const float* x, const int* expert_indices, const float
                           int expert_id, float* gathered, int* token_map, int* count,
                           const MoeConfig* cfg, void* stream) {
     (void)expert_weights;  // unused, as in the reference (naive_moe.cu:358)
-    TRY(check_cfg(cfg, AMDMOE_DTYPE_F32));
+    TRY(check_gate_cfg(cfg));
     AMDMOE_CHECK_ARG(expert_id >= 0 && expert_id < cfg->num_experts, "expert_id=%d out of range", expert_id);
     return launch_gather_one(x, expert_indices, cfg->num_tokens, cfg->top_k, cfg->num_experts,
                              cfg->hidden_dim, expert_id, gathered, token_map, count,
@@ -418,7 +464,7 @@ int amdmoe_moe_permute(const int* expert_indices, const MoeConfig* cfg, int* cou
     const size_t tiles_bytes = align_up(16 * (size_t)(mt + 1), 256);
     const size_t perm_bytes = permute_scratch_bytes(c.num_tokens, c.num_experts);
     void* scratch = nullptr;
-    TRY(cached_workspace(tiles_bytes + 256 + perm_bytes, &scratch));
+    TRY(cached_workspace(tiles_bytes + 256 + perm_bytes, &scratch, SCR_PERMUTE));
     int4* tiles = (int4*)scratch;
     int* nt = (int*)((uint8_t*)scratch + tiles_bytes);
     int* perm = perm_bytes ? (int*)((uint8_t*)scratch + tiles_bytes + 256) : nullptr;
@@ -466,10 +512,14 @@ int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* 
     AMDMOE_CHECK_ARG(c.num_queries >= 0 && c.num_heads >= 0 && c.head_dim_compressed >= 1 &&
                          c.head_dim_positional >= 0 && c.num_selected_kv >= 1,
                      "bad DsaConfig");
+    // scores beyond what LDS holds go to the entry's own cached scratch
+    const size_t need = dsa_f32_scratch_bytes(c.num_queries, c.num_heads, c.num_selected_kv);
+    void* scratch = nullptr;
+    if (need) TRY(cached_workspace(need, &scratch, SCR_DSA_F32));
     return launch_dsa_f32(q_nope, q_pe, kv_cache_compressed, kv_cache_positional, v_cache,
                           sparse_indices, output, c.num_queries, c.num_heads,
                           c.head_dim_compressed, c.head_dim_positional, c.num_selected_kv,
-                          c.total_kv_tokens, (hipStream_t)stream);
+                          c.total_kv_tokens, (float*)scratch, (hipStream_t)stream);
 }
 
 static int dsa_cfg_check(const DsaConfig* cfg) {
@@ -555,10 +605,10 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
     const DsaConfig& c = *cfg;
     AMDMOE_CHECK_ARG(c.num_queries >= 0 && c.num_heads >= 1 && c.num_selected_kv >= 1,
                      "bad DsaConfig");
-    // the token-split partials live in a private buffer of the cached workspace
+    // the token-split partials live in the decode's own cached scratch
     const size_t need = dsa_paged_scratch_bytes(c.num_queries, c.num_heads, c.num_selected_kv);
     void* scratch = nullptr;
-    if (need) TRY(cached_workspace(need, &scratch));
+    if (need) TRY(cached_workspace(need, &scratch, SCR_DSA_DECODE));
     return launch_dsa_bf16_paged(q_nope, q_pe, cache, c.total_kv_tokens, page_table,
                                  logical_indices, output, c.num_queries, c.num_heads,
                                  c.head_dim_compressed,

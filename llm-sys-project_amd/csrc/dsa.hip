@@ -32,6 +32,14 @@
 namespace amdmoe {
 
 // ---------------------------------------------------------------- fp32
+// An index outside [0, N) selects no row: it takes no part in the softmax
+// (score -inf, weight 0) and nothing is read for it, so the result is the
+// attention over the valid indices (0 when there is none).  The scores of
+// one (q,h) row live in LDS for S <= kF32LdsS; beyond that in `gscore`
+// ([Q*H, S] fp32 scratch), with the same arithmetic.
+constexpr int kF32LdsS = 16384;
+
+template <bool GLOBAL>
 __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ qn,
                                                      const float* __restrict__ qp,
                                                      const float* __restrict__ kc,
@@ -39,17 +47,23 @@ __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ q
                                                      const float* __restrict__ v,
                                                      const int* __restrict__ idx,
                                                      float* __restrict__ out, int H, int Dc,
-                                                     int Dp, int S) {
-    extern __shared__ float s_score[];  // [S]
+                                                     int Dp, int S, long N,
+                                                     float* __restrict__ gscore) {
+    extern __shared__ float s_lds[];  // [S] (LDS form)
     const int qh = blockIdx.x;
     const int q = qh / H;
     const int lane = threadIdx.x;
+    float* s_score = GLOBAL ? gscore + (size_t)qh * S : s_lds;
     const float scale = 1.0f / sqrtf((float)(Dc + Dp));
     const float* qnr = qn + (size_t)qh * Dc;
     const float* qpr = qp + (size_t)qh * Dp;
     const int* ir = idx + (size_t)q * S;
     for (int s = lane; s < S; s += 64) {
         const long row = ir[s];
+        if (row < 0 || row >= N) {
+            s_score[s] = -INFINITY;
+            continue;
+        }
         const float* kcr = kc + row * Dc;
         const float* kpr = kp + row * Dp;
         float sc = 0.0f, sp = 0.0f;
@@ -58,9 +72,13 @@ __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ q
         s_score[s] = mul_rn(add_rn(sc, sp), scale);
     }
     __syncthreads();
-    float mx = -FLT_MAX;
+    float mx = -INFINITY;
     for (int s = lane; s < S; s += 64) mx = fmaxf(mx, s_score[s]);
     mx = wave_max(mx);
+    if (mx == -INFINITY) {  // no valid index
+        for (int d = lane; d < Dc; d += 64) out[(size_t)qh * Dc + d] = 0.0f;
+        return;
+    }
     for (int s = lane; s < S; s += 64) s_score[s] = expf(s_score[s] - mx);
     __syncthreads();
     float tot = 0.0f;
@@ -71,19 +89,30 @@ __global__ __launch_bounds__(64) void dsa_f32_kernel(const float* __restrict__ q
     __syncthreads();
     for (int d = lane; d < Dc; d += 64) {
         float acc = 0.0f;
-        for (int s = 0; s < S; s++) acc = mac_rn(acc, s_score[s], v[(long)ir[s] * Dc + d]);
+        for (int s = 0; s < S; s++) {
+            const long row = ir[s];
+            if (row >= 0 && row < N) acc = mac_rn(acc, s_score[s], v[row * Dc + d]);
+        }
         out[(size_t)qh * Dc + d] = acc;
     }
 }
 
+size_t dsa_f32_scratch_bytes(int Q, int H, int S) {
+    return S > kF32LdsS ? (size_t)Q * H * S * 4 : 0;
+}
+
 int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const float* kp,
                    const float* v, const int* idx, float* out, int Q, int H, int Dc, int Dp, int S,
-                   int N, hipStream_t st) {
-    size_t lds = sizeof(float) * (size_t)S;
-    AMDMOE_CHECK_ARG(lds <= 64 * 1024, "dsa_forward: S=%d exceeds 16384", S);
+                   int N, float* scratch, hipStream_t st) {
     if (Q == 0 || H == 0) return AMDMOE_OK;
-    hipLaunchKernelGGL(dsa_f32_kernel, dim3(Q * H), dim3(64), lds, st, qn, qp, kc, kp, v, idx, out,
-                       H, Dc, Dp, S);
+    if (S <= kF32LdsS) {
+        hipLaunchKernelGGL(dsa_f32_kernel<false>, dim3(Q * H), dim3(64), sizeof(float) * (size_t)S, st,
+                           qn, qp, kc, kp, v, idx, out, H, Dc, Dp, S, (long)N, nullptr);
+    } else {
+        AMDMOE_CHECK_ARG(scratch != nullptr, "dsa_forward: no score scratch for S=%d", S);
+        hipLaunchKernelGGL(dsa_f32_kernel<true>, dim3(Q * H), dim3(64), 0, st, qn, qp, kc, kp, v, idx,
+                           out, H, Dc, Dp, S, (long)N, scratch);
+    }
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
@@ -118,7 +147,8 @@ constexpr int kStageB = kTileTok * kRowBytes;    // 36864
 constexpr int kDsaNS = 3;
 constexpr int kMaxS = 4096;
 constexpr int kRowsOff = kDsaNS * kStageB;       // 110592
-constexpr int kDsaLds = kRowsOff + kMaxS * 4;    // 126976
+constexpr int kMaskOff = kRowsOff + kMaxS * 4;   // 126976: validity bits, 64 tokens per word
+constexpr int kDsaLds = kMaskOff + kMaxS / 8;    // 127488
 constexpr int kLoadsPerWave = kStageB / 1024 / 4;  // 9
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -151,18 +181,33 @@ typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 // 256 threads of the block (paged latent cache: logical token i lives in
 // row page_table[i / page] * page + i % page).  All index loads are issued
 // before any page-table load, so the prologue costs two load latencies.
+// A selected token is valid when its logical index lies in [0, seq) (seq =
+// pages_per_seq * page, the page-table row's capacity), its page id is >= 0
+// and its row lies inside the cache; an invalid token (e.g. the -1 padding
+// of a sequence shorter than the selection) reads no page-table entry, gets
+// row -1 and takes no part in the softmax.  Validity of tokens 64b..64b+63
+// goes to bit i of s_mask[b] (wave w of round k writes mask 4k + w).
 template <int N>
 __device__ __forceinline__ void translate_rows(const int* __restrict__ lg, const int* __restrict__ pt,
-                                               int S, int page, int* s_rows) {
+                                               int S, int page, long seq, long cache_rows,
+                                               int* s_rows, unsigned long long* s_mask) {
     const int tid = threadIdx.x;
     int li[N], pg[N];
 #pragma unroll
-    for (int k = 0; k < N; k++) li[k] = tid + 256 * k < S ? lg[tid + 256 * k] : 0;
+    for (int k = 0; k < N; k++) li[k] = tid + 256 * k < S ? lg[tid + 256 * k] : -1;
 #pragma unroll
-    for (int k = 0; k < N; k++) pg[k] = tid + 256 * k < S ? pt[li[k] / page] : 0;
+    for (int k = 0; k < N; k++) {
+        if (li[k] >= seq) li[k] = -1;
+        pg[k] = li[k] >= 0 ? pt[li[k] / page] : -1;
+    }
 #pragma unroll
-    for (int k = 0; k < N; k++)
-        if (tid + 256 * k < S) s_rows[tid + 256 * k] = pg[k] * page + li[k] % page;
+    for (int k = 0; k < N; k++) {
+        const long row = (long)pg[k] * page + (li[k] >= 0 ? li[k] % page : 0);
+        const bool ok = li[k] >= 0 && pg[k] >= 0 && row < cache_rows;
+        if (tid + 256 * k < S) s_rows[tid + 256 * k] = ok ? (int)row : -1;
+        const unsigned long long m = __ballot(ok);
+        if ((tid & 63) == 0) s_mask[4 * k + (tid >> 6)] = m;
+    }
 }
 
 __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
@@ -172,6 +217,7 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
     int pages_per_seq, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int* s_rows = (int*)(smem + kRowsOff);
+    unsigned long long* s_mask = (unsigned long long*)(smem + kMaskOff);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // query-major block order, 4 head groups of one query adjacent: with
@@ -189,7 +235,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
 
     // page-table translation of this query's indices: physical row, or -1
     translate_rows<kMaxS / 256>(logical + (size_t)qi * S, page_table + (size_t)qi * pages_per_seq,
-                                S, page, s_rows);
+                                S, page, (long)pages_per_seq * page, cache_bytes / kRowBytes, s_rows,
+                                s_mask);
 
     // q of my head as B fragments: 18 K-steps of 32 dims, group g holds 8
     u32x4 qf[18];
@@ -265,12 +312,13 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged_kernel(
                 else sa = mfma_bf16(a[ks], qf[ks], sa);
             }
         }
-        // lane: head c16, tokens 16th + 4g + i of this tile
+        // lane: head c16, tokens 16th + 4g + i of this tile (an invalid
+        // token, or one past S, scores -inf)
         float sv[4];
         float tmax = -INFINITY;
+        const uint32_t vmask = (uint32_t)(s_mask[t >> 1] >> (32 * (t & 1) + 16 * th + 4 * g));
         for (int i = 0; i < 4; i++) {
-            const int tk = t * kTileTok + 16 * th + 4 * g + i;
-            sv[i] = tk < S ? (sa[i] + sb2[i]) * scale_log2 : -INFINITY;
+            sv[i] = (vmask >> i) & 1u ? (sa[i] + sb2[i]) * scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, sv[i]);
         }
         tmax = xor16_max(tmax);
@@ -369,7 +417,8 @@ constexpr int kMaxS64 = 2048;
 constexpr int kRows64Off = 2 * kStage64;                   // 147456
 constexpr int kP64Off = kRows64Off + kMaxS64 * 4;          // 155648
 constexpr int kMax64Off = kP64Off + 4 * 1024;              // 159744
-constexpr int kDsa64Lds = kMax64Off + 4 * 32 * 4;          // 160256
+constexpr int kMask64Off = kMax64Off + 4 * 32 * 4;         // 160256: validity bits per tile
+constexpr int kDsa64Lds = kMask64Off + kMaxS64 / 8;        // 160512
 
 __device__ __forceinline__ int tile64_off(int t, int j) {  // token t (0..63), chunk j (0..71)
     return ((t >> 4) * 18 + (j >> 2)) * 1024 + (t & 15) * 64 + ((j & 3) ^ ((t >> 2) & 3)) * 16;
@@ -384,6 +433,7 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
     int* s_rows = (int*)(smem + kRows64Off);
     uint16_t* s_p = (uint16_t*)(smem + kP64Off);    // [ht][head 16][token 64] bf16
     float* s_max = (float*)(smem + kMax64Off);      // [wave][32 heads]
+    unsigned long long* s_mask = (unsigned long long*)(smem + kMask64Off);  // [tile] token bits
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // XCD remap as in dsa_bf16_paged_kernel: a query's head groups share an XCD
@@ -396,7 +446,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
     const int g = lane >> 4, c16 = lane & 15;
 
     translate_rows<kMaxS64 / 256>(logical + (size_t)qi * S, page_table + (size_t)qi * pages_per_seq,
-                                  S, page, s_rows);
+                                  S, page, (long)pages_per_seq * page, cache_bytes / kRowBytes,
+                                  s_rows, s_mask);
     // q of heads h0 + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
     u32x4 qf[2][18];
 #pragma unroll
@@ -420,7 +471,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
     // shift the LDS destination.
     auto tile_vo = [&](int tile) {
         const int tok = tile * kT64 + my_tok;
-        return tok < S ? (uint32_t)((long)s_rows[tok] * kRowBytes + 16 * my_chunk) : kOobDsa;
+        const int r = tok < S ? s_rows[tok] : -1;
+        return r >= 0 ? (uint32_t)((long)r * kRowBytes + 16 * my_chunk) : kOobDsa;
     };
     auto issue_n = [&](int st, uint32_t vo, int n) __attribute__((always_inline)) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -486,13 +538,13 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
             }
         }
         float sv[2][4], tm[2];
+        const uint32_t vmask = (uint32_t)(s_mask[t] >> (16 * wave + 4 * g));  // invalid: -inf
 #pragma unroll
         for (int ht = 0; ht < 2; ht++) {
             tm[ht] = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int tk = t * kT64 + 16 * wave + 4 * g + i;
-                sv[ht][i] = tk < S ? (sacc[ht][0][i] + sacc[ht][1][i]) * scale_log2 : -INFINITY;
+                sv[ht][i] = (vmask >> i) & 1u ? (sacc[ht][0][i] + sacc[ht][1][i]) * scale_log2 : -INFINITY;
                 tm[ht] = fmaxf(tm[ht], sv[ht][i]);
             }
             tm[ht] = xor32_max(xor16_max(tm[ht]));
@@ -629,7 +681,8 @@ constexpr int kStage32 = kT32 * kRowBytes;                // 36864
 constexpr int kRing32 = 4;
 constexpr int kMaxChunk = 2048;                           // tokens per split
 constexpr int kRows32Off = kRing32 * kStage32;            // 147456
-constexpr int kDsaSplitLds = kRows32Off + kMaxChunk * 4;  // 155648
+constexpr int kMask32Off = kRows32Off + kMaxChunk * 4;    // 155648: validity bits, 64 tokens per word
+constexpr int kDsaSplitLds = kMask32Off + kMaxChunk / 8;  // 155904
 
 __device__ __forceinline__ int hsw(int a) { return ((a & 1) << 1) | (a >> 1); }
 __device__ __forceinline__ int tile32_off(int t, int j) {  // token t (0..31), chunk j (0..71)
@@ -682,6 +735,7 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int* s_rows = (int*)(smem + kRows32Off);
+    unsigned long long* s_mask = (unsigned long long*)(smem + kMask32Off);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // work item lin = (query, head group, split), dealt to the 8 XCDs in
@@ -704,7 +758,10 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     // the page-table translation: logical indices, then page-table entries,
     // then q (36 loads per lane), then wait for all but the q loads.  The
     // q loads are waited for (by the compiler) at tile 0's first S step.
-    // An index outside the sequence gives row -1: a zero row.
+    // A token is valid when its logical index lies in [0, pages_per_seq *
+    // page), its page id is >= 0 and its row inside the cache; an invalid
+    // one (e.g. the -1 padding of a sequence shorter than the selection)
+    // reads no page-table entry, loads a zero row and scores -inf.
     constexpr int kRowsPer = kMaxChunk / 256;
     int li[kRowsPer], pg[kRowsPer];
     {
@@ -717,7 +774,7 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
         for (int k = 0; k < kRowsPer; k++) {
             const bool ok = li[k] >= 0 && li[k] < seq;
             if (!ok) li[k] = -1;
-            pg[k] = ok ? pt[li[k] / page] : 0;
+            pg[k] = ok ? pt[li[k] / page] : -1;
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -735,10 +792,19 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     }
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<36>();  // every page-table entry has arrived
+    {
+        const long cache_rows = cache_bytes / kRowBytes;
 #pragma unroll
-    for (int k = 0; k < kRowsPer; k++)
-        if (tid + 256 * k < len) s_rows[tid + 256 * k] = li[k] >= 0 ? pg[k] * page + li[k] % page : -1;
-    lds_barrier();  // s_rows visible (the q loads stay in flight)
+        for (int k = 0; k < kRowsPer; k++) {
+            const long row = (long)pg[k] * page + (li[k] >= 0 ? li[k] % page : 0);
+            const bool ok = li[k] >= 0 && pg[k] >= 0 && row < cache_rows;
+            if (tid + 256 * k < len) s_rows[tid + 256 * k] = ok ? (int)row : -1;
+            // validity of split tokens 64(4k + w) .. +63 (none past len)
+            const unsigned long long m = __ballot(ok);
+            if (lane == 0) s_mask[4 * k + wave] = m;
+        }
+    }
+    lds_barrier();  // s_rows, s_mask visible (the q loads stay in flight)
 
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
     // DMA: block b of a tile is filled by one instruction, lane l taking
@@ -848,8 +914,10 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
-        // lane: head 16ht + c16, tokens 16tt + 4g + i of the tile
+        // lane: head 16ht + c16, tokens 16tt + 4g + i of the tile; an
+        // invalid token (or one past the split) scores -inf
         float sv[2][2][4], tm[2];
+        const uint32_t vmask = (uint32_t)(s_mask[t >> 1] >> (32 * (t & 1) + 4 * g));
 #pragma unroll
         for (int ht = 0; ht < 2; ht++) {
             tm[ht] = -INFINITY;
@@ -857,13 +925,14 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int tk = kT32 * t + 16 * tt + 4 * g + i;
-                    sv[tt][ht][i] = tk < len ? sacc[tt][ht][i] * scale_log2 : -INFINITY;
+                    sv[tt][ht][i] = (vmask >> (16 * tt + i)) & 1u ? sacc[tt][ht][i] * scale_log2 : -INFINITY;
                     tm[ht] = fmaxf(tm[ht], sv[tt][ht][i]);
                 }
             tm[ht] = xor32_max(xor16_max(tm[ht]));
         }
-        const bool first = m_run[0] == -INFINITY;  // uniform: tile 0 (it has a live token)
+        // uniform: no valid token so far (validity is per token, the same
+        // for every head, so all heads' maxima are finite or none is)
+        const bool first = m_run[0] == -INFINITY;
         const bool raise = tm[0] > m_run[0] + 8.0f || tm[1] > m_run[1] + 8.0f;
         if (first) {
             m_run[0] = tm[0];
@@ -890,12 +959,14 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
 #pragma unroll
         for (int ht = 0; ht < 2; ht++) {
             float p[2][4];
+            // with no valid token yet every score is -inf: subtract 0, not -inf
+            const float m_use = m_run[ht] == -INFINITY ? 0.0f : m_run[ht];
 #pragma unroll
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     // the hardware exp2 (0 for a masked -inf score)
-                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][ht][i] - m_run[ht]);
+                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][ht][i] - m_use);
                     l_lane[ht] += p[tt][i];
                 }
             pb[ht] = (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),

@@ -201,14 +201,16 @@ __device__ __forceinline__ int count_below(unsigned long long m) {
 template <int kPer>  // positions per thread: max_seq <= 1024 * kPer
 __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float* __restrict__ scores,
                                                                     const int* __restrict__ seq_len,
-                                                                    int max_seq, int topk,
+                                                                    int max_seq, int cap, int topk,
                                                                     int* __restrict__ out) {
     constexpr int kWaves = kTopkThreads / 64;
     __shared__ __align__(16) int s_hist[kWaves][256];  // one histogram per wave
     __shared__ unsigned s_slice[kPer + 1];             // counts before each slice, total
     __shared__ int s_sel[2];                           // digit, remaining count
     const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = min(seq_len[qi], max_seq);
+    // the positions the scoring kernel scored: seq_len, at most max_seq
+    // and the page-table row's capacity (cap = min of the two)
+    const int n = max(0, min(seq_len[qi], cap));
     const float* row = scores + (size_t)qi * max_seq;
     // histogram passes: position j * 1024 + tid in key[j], so the 64 lanes
     // of a wave hold 64 unrelated positions
@@ -411,9 +413,10 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
     AMDMOE_LAUNCH_CHECK();
     // registers hold ceil(max_seq / 1024) keys per thread, rounded up to a power of two
     const int per = (max_seq + kTopkThreads - 1) / kTopkThreads;
+    const int cap = (int)std::min<long>(max_seq, (long)pages_per_seq * page);
 #define AMDMOE_TOPK_LAUNCH(P)                                                                     \
     hipLaunchKernelGGL(indexer_topk_kernel<P>, dim3((unsigned)Q), dim3(kTopkThreads), 0, st, scores, \
-                       seq_len, max_seq, topk, out)
+                       seq_len, max_seq, cap, topk, out)
     if (per <= 1) AMDMOE_TOPK_LAUNCH(1);
     else if (per <= 2) AMDMOE_TOPK_LAUNCH(2);
     else if (per <= 4) AMDMOE_TOPK_LAUNCH(4);

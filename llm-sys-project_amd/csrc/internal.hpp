@@ -68,6 +68,13 @@ int launch_quant_weight(const float* w, long rows, int cols, const float* u, uin
 long max_mtiles(long P, int E);
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
 
+// moe_generic.hip: fp32 UP + DOWN + combine for any D and I (the forward's
+// tail when D or I is not a multiple of 32), over the permutation's M-tiles
+int launch_experts_f32_any(const float* x, const float* w1, const float* w2, int T, int E, int K,
+                           int D, int I, const int4* tiles, const int* num_tiles, long max_tiles,
+                           const int* sorted_token, const int* sorted_slot, const float* sorted_w,
+                           const int* idx, float* act, float* ypair, float* y, hipStream_t st);
+
 // moe_pack.hip: [E][N][K]-byte weights -> fragment-block order (N % 16 == 0,
 // K % 128 == 0)
 int launch_pack_weights(const uint8_t* w, long E, long N, long K, uint8_t* out, hipStream_t st);
@@ -83,9 +90,12 @@ int launch_scatter_f32(const float* expert_out, const int* token_map, const floa
                        hipStream_t st);
 
 // dsa.hip
+// scratch: dsa_f32_scratch_bytes(Q, H, S) bytes of fp32 scores (0 bytes /
+// nullptr when the scores fit in LDS)
+size_t dsa_f32_scratch_bytes(int Q, int H, int S);
 int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const float* kp,
                    const float* v, const int* idx, float* out, int Q, int H, int Dc, int Dp, int S,
-                   int N, hipStream_t st);
+                   int N, float* scratch, hipStream_t st);
 // scratch: dsa_paged_scratch_bytes(Q, H, S) bytes (split partials), may be
 // 0 bytes / nullptr when that is 0
 size_t dsa_paged_scratch_bytes(int Q, int H, int S);

@@ -66,12 +66,12 @@ def lib():
             "orc_dsa_output_proj": (None, [_f32p, _f32p, _f32p, _I, _I, _I, _I]),
             "orc_dsa_forward_f32": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p, _f32p,
                                            _I, _I, _I, _I, _I]),
-            "orc_dsa_translate": (None, [_i32p, _i32p, _I, _I, _I, _I, _i32p]),
+            "orc_dsa_translate": (None, [_i32p, _i32p, _I, _I, _I, _I, _L, _i32p]),
             "orc_dsa_decode_bf16_paged": (None, [_u16p, _u16p, _u16p, _i32p, _i32p, _f32p,
-                                                 _I, _I, _I, _I, _I, _I, _I]),
+                                                 _I, _I, _I, _I, _I, _I, _I, _L]),
             "orc_dsa_indexer_scores": (None, [_u8p, _f32p, _f32p, _u8p, _f32p, _i32p, _i32p,
                                               _I, _I, _I, _I, _I, _f32p]),
-            "orc_dsa_indexer_topk": (None, [_f32p, _i32p, _I, _I, _I, _i32p]),
+            "orc_dsa_indexer_topk": (None, [_f32p, _i32p, _I, _I, _I, _I, _i32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -328,16 +328,21 @@ def dsa_output_proj(attn, v):
     return out
 
 
-def dsa_translate(logical, page_table, page):
+def dsa_translate(logical, page_table, page, cache_rows=0):
+    """Physical cache row of each selected logical index, -1 where it selects
+    nothing (index outside the page-table row, negative page id, row at or
+    past cache_rows when cache_rows > 0)."""
     logical = _c(logical, np.int32)
     pt = _c(page_table, np.int32)
     Q, S = logical.shape
     out = np.empty((Q, S), np.int32)
-    lib().orc_dsa_translate(logical, pt, Q, S, pt.shape[1], page, out)
+    lib().orc_dsa_translate(logical, pt, Q, S, pt.shape[1], page, cache_rows, out)
     return out
 
 
 def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, Dc, page):
+    """Paged decode over the valid selected tokens only (see dsa_translate);
+    0 for a query with none."""
     qn, qp, cache = (_c(a, np.uint16) for a in (qn, qp, cache))
     pt = _c(page_table, np.int32)
     logical = _c(logical, np.int32)
@@ -346,7 +351,7 @@ def dsa_decode_bf16_paged(qn, qp, cache, page_table, logical, Dc, page):
     S = logical.shape[1]
     out = np.empty((Q, H, Dc), np.float32)
     lib().orc_dsa_decode_bf16_paged(qn, qp, cache, pt, logical, out, Q, H, Dc, Dp, S,
-                                    pt.shape[1], page)
+                                    pt.shape[1], page, cache.shape[0])
     return out
 
 
@@ -364,12 +369,13 @@ def dsa_indexer_scores(qc, qs, hw, kc, ks, page_table, seq_len, page, max_seq):
     return out
 
 
-def dsa_indexer_topk(scores, seq_len, topk):
+def dsa_indexer_topk(scores, seq_len, topk, cap=0):
     """The topk positions per row by score (ties: lower position), in
-    ascending position order, padded with -1."""
+    ascending position order, padded with -1; a row holds min(seq_len, cap)
+    candidate positions (cap <= 0: the row length)."""
     scores = _c(scores, np.float32)
     sl = _c(seq_len, np.int32)
     Q, max_seq = scores.shape
     out = np.empty((Q, topk), np.int32)
-    lib().orc_dsa_indexer_topk(scores, sl, Q, max_seq, topk, out)
+    lib().orc_dsa_indexer_topk(scores, sl, Q, max_seq, cap, topk, out)
     return out

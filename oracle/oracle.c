@@ -594,24 +594,38 @@ EXPORT void orc_dsa_output_proj(const float* attn, const float* v, float* out,
 /* Paged address translation (BASELINE DSA config; the reference has no page
  * table): logical index i of query q lives at physical token
  * page_table[q][i / page] * page + i % page. */
+/* Physical row of a selected token, or -1 when it selects nothing: logical
+ * index outside [0, pages_per_seq * page), a negative page id, or a row at
+ * or past cache_rows (cache_rows <= 0: unbounded). */
+static long dsa_phys_row(const int* pt_row, int i, int pages_per_seq, int page, long cache_rows) {
+    if (i < 0 || (long)i >= (long)pages_per_seq * page) return -1;
+    int pg = pt_row[i / page];
+    if (pg < 0) return -1;
+    long row = (long)pg * page + i % page;
+    if (cache_rows > 0 && row >= cache_rows) return -1;
+    return row;
+}
+
 EXPORT void orc_dsa_translate(const int* logical, const int* page_table, int Q, int S,
-                              int pages_per_seq, int page, int* physical) {
+                              int pages_per_seq, int page, long cache_rows, int* physical) {
     for (int q = 0; q < Q; q++)
-        for (int s = 0; s < S; s++) {
-            int i = logical[(size_t)q * S + s];
-            physical[(size_t)q * S + s] =
-                page_table[(size_t)q * pages_per_seq + i / page] * page + i % page;
-        }
+        for (int s = 0; s < S; s++)
+            physical[(size_t)q * S + s] = (int)dsa_phys_row(
+                page_table + (size_t)q * pages_per_seq, logical[(size_t)q * S + s], pages_per_seq,
+                page, cache_rows);
 }
 
 /* bf16 paged MLA-absorbed decode: one latent cache [Ntok, Dc+Dp] bf16 whose
  * first Dc columns are K_c and also V, last Dp columns K_p.  Math as
- * orc_dsa_forward_f32 on the decoded values; out fp32 [Q, H, Dc]. */
+ * orc_dsa_forward_f32 on the decoded values; out fp32 [Q, H, Dc].  Selected
+ * tokens that select nothing (dsa_phys_row == -1, e.g. the -1 padding of a
+ * sequence shorter than the selection) are left out: the softmax runs over
+ * the valid tokens only, in their order, and a query with none gets 0. */
 EXPORT void orc_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                       const uint16_t* cache, const int* page_table,
                                       const int* logical, float* output,
                                       int Q, int H, int Dc, int Dp, int S,
-                                      int pages_per_seq, int page) {
+                                      int pages_per_seq, int page, long cache_rows) {
     int Dt = Dc + Dp;
     float scale = 1.0f / sqrtf((float)(Dc + Dp));
     #pragma omp parallel for schedule(dynamic)
@@ -621,26 +635,34 @@ EXPORT void orc_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_
         float* scores = (float*)malloc(sizeof(float) * (size_t)S);
         float* qn = (float*)malloc(sizeof(float) * (size_t)Dc);
         float* qp = (float*)malloc(sizeof(float) * (size_t)(Dp > 0 ? Dp : 1));
+        int nv = 0;  /* valid tokens, compacted in selection order */
         for (int s = 0; s < S; s++) {
-            int i = logical[(size_t)q * S + s];
-            long phys = (long)page_table[(size_t)q * pages_per_seq + i / page] * page + i % page;
+            long phys = dsa_phys_row(page_table + (size_t)q * pages_per_seq,
+                                     logical[(size_t)q * S + s], pages_per_seq, page, cache_rows);
+            if (phys < 0) continue;
             const uint16_t* row = cache + phys * Dt;
-            for (int d = 0; d < Dc; d++) kc[(size_t)s * Dc + d] = orc_bf16_to_f32(row[d]);
-            for (int d = 0; d < Dp; d++) kp[(size_t)s * Dp + d] = orc_bf16_to_f32(row[Dc + d]);
+            for (int d = 0; d < Dc; d++) kc[(size_t)nv * Dc + d] = orc_bf16_to_f32(row[d]);
+            for (int d = 0; d < Dp; d++) kp[(size_t)nv * Dp + d] = orc_bf16_to_f32(row[Dc + d]);
+            nv++;
+        }
+        if (nv == 0) {
+            memset(output + (size_t)q * H * Dc, 0, sizeof(float) * (size_t)H * Dc);
+            free(kc); free(kp); free(scores); free(qn); free(qp);
+            continue;
         }
         for (int h = 0; h < H; h++) {
             for (int d = 0; d < Dc; d++) qn[d] = orc_bf16_to_f32(q_nope[((size_t)q * H + h) * Dc + d]);
             for (int d = 0; d < Dp; d++) qp[d] = orc_bf16_to_f32(q_pe[((size_t)q * H + h) * Dp + d]);
-            for (int s = 0; s < S; s++) {
+            for (int s = 0; s < nv; s++) {
                 float sum_c = 0.0f, sum_p = 0.0f;
                 for (int d = 0; d < Dc; d++) sum_c += qn[d] * kc[(size_t)s * Dc + d];
                 for (int d = 0; d < Dp; d++) sum_p += qp[d] * kp[(size_t)s * Dp + d];
                 scores[s] = (sum_c + sum_p) * scale;
             }
-            orc_softmax(scores, S);
+            orc_softmax(scores, nv);
             for (int d = 0; d < Dc; d++) {
                 float sum = 0.0f;
-                for (int s = 0; s < S; s++) sum += scores[s] * kc[(size_t)s * Dc + d];
+                for (int s = 0; s < nv; s++) sum += scores[s] * kc[(size_t)s * Dc + d];
                 output[((size_t)q * H + h) * Dc + d] = sum;
             }
         }
@@ -670,8 +692,10 @@ EXPORT void orc_dsa_indexer_scores(const uint8_t* qc, const float* qs, const flo
             wq[j] = (double)hw[(size_t)q * Hi + j] * (double)qs[(size_t)q * Hi + j];
             for (int d = 0; d < 128; d++) qv[(size_t)j * 128 + d] = orc_e4m3_to_f32(qc[((size_t)q * Hi + j) * 128 + d]);
         }
+        /* positions past seq_len or past the page-table row's capacity score -inf */
+        long len = seq_len[q] < (long)pages_per_seq * page ? seq_len[q] : (long)pages_per_seq * page;
         for (int s = 0; s < max_seq; s++) {
-            if (s >= seq_len[q]) { scores[(size_t)q * max_seq + s] = -INFINITY; continue; }
+            if (s >= len) { scores[(size_t)q * max_seq + s] = -INFINITY; continue; }
             long row = (long)page_table[(size_t)q * pages_per_seq + s / page] * page + s % page;
             for (int d = 0; d < 128; d++) qf[d] = orc_e4m3_to_f32(kc[row * 128 + d]);
             double tot = 0.0;
@@ -700,10 +724,13 @@ static int cmp_score_desc(const void* a, const void* b) {
     return i - j;
 }
 EXPORT void orc_dsa_indexer_topk(const float* scores, const int* seq_len, int Q, int max_seq,
-                                 int topk, int* out) {
+                                 int cap, int topk, int* out) {
+    /* cap: positions scored per row (the page-table row's capacity), <= 0: max_seq */
     int* pos = (int*)malloc(sizeof(int) * (size_t)(max_seq > 0 ? max_seq : 1));
+    int lim = cap > 0 && cap < max_seq ? cap : max_seq;
     for (int q = 0; q < Q; q++) {
-        int n = seq_len[q] < max_seq ? seq_len[q] : max_seq;
+        int n = seq_len[q] < lim ? seq_len[q] : lim;
+        if (n < 0) n = 0;
         for (int s = 0; s < n; s++) pos[s] = s;
         g_topk_row = scores + (size_t)q * max_seq;
         g_topk_len = n;

@@ -125,3 +125,137 @@ def test_dsa_bf16_paged_split_max_jumps(amd, orc):
     err = _paged_case(amd, orc, Q, H, S, ctx, page=page, check_q=[0, 31, 63],
                       inputs=(qn, qp, cache, pt, logical, pps))
     assert err < 1e-2
+
+
+# ------------------------------------------------------------------ invalid indices
+def _invalid_mix(logical, pt, ctx, page, rng, all_invalid_q=None):
+    """Plants the index forms that select nothing: -1 padding at the end of a
+    row (as the indexer emits for a sequence shorter than the selection),
+    indices at or past the page-table row's capacity, and a page-table entry
+    of -1 (an unmapped page) or past the cache's last page under some
+    selected positions."""
+    lg = logical.copy()
+    pt = pt.copy()
+    Q, S = lg.shape
+    n_pages = pt.size
+    for q in range(Q):
+        npad = rng.integers(0, max(1, S // 3) + 1)
+        if npad:
+            lg[q, S - npad:] = -1
+        if S > 4:
+            lg[q, rng.integers(0, S - npad if S - npad > 0 else 1)] = ctx + rng.integers(0, 5 * page)
+        if pt.shape[1] > 1:
+            pt[q, rng.integers(0, pt.shape[1])] = -1
+            pt[q, rng.integers(0, pt.shape[1])] = n_pages + rng.integers(0, 100)
+    if all_invalid_q is not None:
+        lg[all_invalid_q, :] = -1
+    return lg, pt
+
+
+@pytest.mark.parametrize("Q,H,S,ctx", [
+    (6, 128, 300, 1024),   # the token-split kernel (H % 128 == 0)
+    (5, 64, 200, 1024),    # one workgroup per 32 heads, 64-token tiles (S <= 2048)
+    (3, 32, 2500, 4096),   # one workgroup per 32 heads, 32-token tiles (S > 2048)
+])
+def test_dsa_bf16_paged_invalid_indices(amd, orc, Q, H, S, ctx):
+    """Selected positions that select nothing take no part in the softmax:
+    the output equals attention over the valid positions only (the oracle's
+    decode, which leaves them out), and a query with no valid position
+    gets 0.  Covers all three decode kernels."""
+    import synth
+    print(f"dsa_bf16 invalid indices Q={Q} H={H} S={S}", flush=True)
+    page = 64
+    qn, qp, cache, pt, logical, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=Q * 7 + S)
+    rng = np.random.default_rng(S)
+    lg, ptn = _invalid_mix(logical.cpu().numpy(), pt.cpu().numpy(), ctx, page, rng, all_invalid_q=1)
+    out = torch.full((Q, H, 512), 0x7fc0, dtype=torch.int16, device="cuda")
+    amd.dsa_decode_bf16_paged(qn, qp, cache, dev(ptn), dev(lg), out,
+                              amd.dsa_config(Q, H, 512, 64, S, page, cache.shape[0]), pps)
+    torch.cuda.synchronize()
+    h = lambda t: t.cpu().numpy().view(np.uint16)
+    ref = orc.dsa_decode_bf16_paged(h(qn), h(qp), h(cache), ptn, lg, 512, page)
+    got = orc.bf16_to_f32(h(out))
+    assert np.isfinite(got).all()
+    assert (got[1] == 0).all()
+    err = np.abs(got - ref).max()
+    print(f"invalid indices H={H}: max_err={err:.3e}")
+    assert err < 1e-2
+
+
+def test_dsa_bf16_paged_invalid_matches_compacted(amd):
+    """GPU against GPU: a row with invalid positions interleaved gives the
+    same output as the row holding only its valid positions (padded with -1
+    at the end), on the split kernel."""
+    import synth
+    print("dsa_bf16 invalid == compacted", flush=True)
+    Q, H, S, ctx, page = 4, 128, 256, 2048, 64
+    qn, qp, cache, pt, logical, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=77)
+    lg = logical.cpu().numpy()
+    holes = lg.copy()
+    holes[:, ::3] = -1
+    comp = np.full_like(lg, -1)
+    for q in range(Q):
+        v = holes[q][holes[q] >= 0]
+        comp[q, :len(v)] = v
+    cfg = amd.dsa_config(Q, H, 512, 64, S, page, cache.shape[0])
+    o1 = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
+    o2 = torch.empty_like(o1)
+    amd.dsa_decode_bf16_paged(qn, qp, cache, pt, dev(holes), o1, cfg, pps)
+    amd.dsa_decode_bf16_paged(qn, qp, cache, pt, dev(comp), o2, cfg, pps)
+    torch.cuda.synchronize()
+    a = o1.cpu().numpy().view(np.uint16)
+    b = o2.cpu().numpy().view(np.uint16)
+    # different tile/split boundaries: equal to bf16 rounding of fp32 sums
+    import oracle
+    d = np.abs(oracle.bf16_to_f32(a) - oracle.bf16_to_f32(b)).max()
+    assert d < 1e-2
+
+
+def test_dsa_f32_invalid_indices(amd, orc):
+    """dsa_forward_f32: an index outside [0, N) selects nothing; the result
+    equals the reference computation on the valid indices only (in order),
+    and a query with none gets 0."""
+    Q, H, Dc, Dp, S, N = 4, 8, 64, 16, 96, 512
+    print("dsa_f32 invalid indices", flush=True)
+    qn, qp, kc, kp, v, idx = orc.reference_dsa_inputs(Q, H, Dc, Dp, S, 64, N)
+    idx = idx.copy()
+    idx[0, ::5] = -1
+    idx[2, 7] = N
+    idx[2, 40] = N + 1000
+    idx[3, :] = -3
+    out = torch.full((Q, H, Dc), float("nan"), dtype=torch.float32, device="cuda")
+    amd.dsa_forward_f32(dev(qn), dev(qp), dev(kc), dev(kp), dev(v), dev(idx), out,
+                        amd.dsa_config(Q, H, Dc, Dp, S, 64, N))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for q in range(Q):
+        valid = idx[q][(idx[q] >= 0) & (idx[q] < N)]
+        if len(valid) == 0:
+            assert (got[q] == 0).all()
+            continue
+        ref = orc.dsa_forward_f32(qn[q:q + 1], qp[q:q + 1], kc, kp, v, valid[None, :].astype(np.int32))
+        np.testing.assert_array_equal(got[q], ref[0])
+
+
+def test_dsa_f32_beyond_lds_s20000(amd, orc):
+    """S = 20000 selected rows (past what one workgroup's LDS holds; the
+    scores go through scratch) with Dc = 48, Dp = 8: equal to the oracle
+    within the reference's largest-case tolerance, and bit-identical per
+    (q, h) to the same arithmetic (the kernel keeps the reference's order)."""
+    Q, H, Dc, Dp, S, N = 2, 3, 48, 8, 20000, 30000
+    print("dsa_f32 S=20000", flush=True)
+    rng = np.random.default_rng(20000)
+    qn = rng.uniform(-0.3, 0.3, (Q, H, Dc)).astype(np.float32)
+    qp = rng.uniform(-0.3, 0.3, (Q, H, Dp)).astype(np.float32)
+    kc = rng.uniform(-0.3, 0.3, (N, Dc)).astype(np.float32)
+    kp = rng.uniform(-0.3, 0.3, (N, Dp)).astype(np.float32)
+    v = rng.uniform(-0.3, 0.3, (N, Dc)).astype(np.float32)
+    idx = np.stack([np.sort(rng.choice(N, S, replace=False)) for _ in range(Q)]).astype(np.int32)
+    ref = orc.dsa_forward_f32(qn, qp, kc, kp, v, idx)
+    out = torch.full((Q, H, Dc), float("nan"), dtype=torch.float32, device="cuda")
+    amd.dsa_forward_f32(dev(qn), dev(qp), dev(kc), dev(kp), dev(v), dev(idx), out,
+                        amd.dsa_config(Q, H, Dc, Dp, S, 64, N))
+    torch.cuda.synchronize()
+    err = np.abs(out.cpu().numpy() - ref).max()
+    print(f"S=20000: max_err={err:.3e}")
+    assert err < 1e-6

@@ -184,3 +184,72 @@ def test_gpu_indexer_feeds_paged_decode(amd, orc):
                                     h(cache).view(np.uint16), h(pt), gi, 512, page)
     got = orc.bf16_to_f32(h(out).view(np.uint16))
     assert np.abs(got - ref).max() < 1e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("H", [128, 64])
+def test_gpu_indexer_short_sequences_feed_paged_decode(amd, orc, H):
+    """Sequences shorter than the selection (seq_len < top-k): the indexer
+    lists all their positions, then -1; the decode takes the -1 padding as
+    selecting nothing, so its output equals attention over the valid
+    positions only.  H=128 runs the token-split decode, H=64 the one-block-
+    per-32-heads decode."""
+    import torch
+    import synth
+    Q, Hi, ctx, page, topk = 4, 64, 2048, 64, 512
+    print(f"indexer (short sequences) -> decode H={H}", flush=True)
+    qn, qp, cache, pt, _, pps = synth.dsa_paged(Q, H, 512, 64, topk, page, ctx, seed=33 + H)
+    qc, qs, hw, kc, ks, _ = synth.dsa_indexer(Q, Hi, ctx, page, seed=34, page_table=pt)
+    seq = [100, 511, 1, ctx]
+    sl = torch.tensor(seq, dtype=torch.int32, device="cuda")
+    scores = torch.empty((Q, ctx), dtype=torch.float32, device="cuda")
+    idx = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    amd.dsa_indexer_topk_fp8(qc, qs, hw, kc, ks, pt, sl, page, ctx, topk, scores, idx)
+    out = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
+    cfg = amd.dsa_config(Q, H, 512, 64, topk, page, cache.shape[0])
+    amd.dsa_decode_bf16_paged(qn, qp, cache, pt, idx, out, cfg, pps)
+    torch.cuda.synchronize()
+    h = lambda t: t.cpu().numpy()
+    gi = h(idx)
+    for q, n in enumerate(seq):
+        m = min(n, topk)
+        assert (gi[q, :m] >= 0).all() and (gi[q, m:] == -1).all()
+        if n <= topk:
+            np.testing.assert_array_equal(gi[q, :m], np.arange(m))
+    np.testing.assert_array_equal(gi, orc.dsa_indexer_topk(h(scores), h(sl), topk))
+    ref = orc.dsa_decode_bf16_paged(h(qn).view(np.uint16), h(qp).view(np.uint16),
+                                    h(cache).view(np.uint16), h(pt), gi, 512, page)
+    got = orc.bf16_to_f32(h(out).view(np.uint16))
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref).max()
+    print(f"short sequences H={H}: max_err={err:.3e}")
+    assert err < 1e-2
+
+
+@pytest.mark.gpu
+def test_gpu_indexer_seq_len_past_page_table_capacity(amd, orc):
+    """seq_len larger than the page-table row's capacity (pages_per_seq *
+    page < max_seq): positions past the capacity are neither scored nor
+    selected, so a row with fewer scored positions than top-k is padded with
+    -1 instead of listing -inf positions."""
+    import torch
+    import synth
+    Q, Hi, ctx, page, topk = 2, 32, 1024, 64, 512
+    print("indexer seq_len past capacity", flush=True)
+    qc, qs, hw, kc, ks, pt = synth.dsa_indexer(Q, Hi, ctx, page, seed=35)
+    pt_small = pt[:, :4].contiguous()            # capacity 256 positions
+    max_seq = ctx
+    sl = torch.tensor([ctx, 300], dtype=torch.int32, device="cuda")
+    scores = torch.empty((Q, max_seq), dtype=torch.float32, device="cuda")
+    idx = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    amd.dsa_indexer_topk_fp8(qc, qs, hw, kc, ks, pt_small, sl, page, max_seq, topk, scores, idx)
+    torch.cuda.synchronize()
+    h = lambda t: t.cpu().numpy()
+    gi = h(idx)
+    for q in range(Q):
+        np.testing.assert_array_equal(gi[q, :256], np.arange(256))
+        assert (gi[q, 256:] == -1).all()
+    assert np.isneginf(h(scores)[:, 256:]).all()
+    ref_sc = orc.dsa_indexer_scores(h(qc), h(qs), h(hw), h(kc), h(ks), h(pt_small), h(sl), page, max_seq)
+    assert np.isneginf(ref_sc[:, 256:]).all()
+    np.testing.assert_array_equal(gi, orc.dsa_indexer_topk(ref_sc, h(sl), topk, cap=256))

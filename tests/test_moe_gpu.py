@@ -502,3 +502,248 @@ def test_forward_fp8_packed_bit_identical_dsv3_t4096(amd, dsv3):
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)
     del p1, p2
+
+
+# ------------------------------------------------------------------ controlled routing
+# Rows per expert chosen so that the grouped GEMM meets every live
+# token-tile count of its fp8 main loop (R = 1..16 tiles of 16 rows, both
+# register-ring depths: R <= 12 and R > 12), row counts on and just past
+# 16-row boundaries, and experts split into two and three M-tiles (more than
+# 256 and 512 rows; the permutation splits them evenly into whole 16-row
+# tiles).
+ROUTED_COUNTS = ([16 * r - 7 for r in range(1, 17)] + [16 * r for r in range(1, 17)]
+                 + [1, 2, 15, 17, 255, 257, 270, 300, 400, 511, 512, 513, 600])
+
+
+def _mtile_rows(cnt, bm=256):
+    """Rows of the M-tiles of an expert with cnt rows (the permutation's
+    split: ceil(cnt/256) tiles of whole 16-row tiles, as even as possible)."""
+    nt = -(-cnt // bm)
+    q = -(-cnt // 16)
+    base, extra = divmod(q, nt)
+    out, first = [], 0
+    for j in range(nt):
+        r = min(16 * (base + (1 if j < extra else 0)), cnt - first)
+        out.append(r)
+        first += r
+    return out
+
+
+def _routed_layout(counts, E, K):
+    """Token -> experts assignment giving expert i exactly counts[i] rows
+    (experts 0..len(counts)-1; the slots left over to make T*K go one each to
+    the following experts).  Slots sorted by expert are dealt to tokens
+    round-robin (slot j -> token j % T), so an expert never sees one token
+    twice as long as its count is at most T."""
+    slots = [e for e, c in enumerate(counts) for _ in range(c)]
+    T = max(max(counts), -(-len(slots) // K))
+    fill = T * K - len(slots)
+    assert len(counts) + fill <= E
+    slots += list(range(len(counts), len(counts) + fill))
+    chosen = [[] for _ in range(T)]
+    for j, e in enumerate(slots):
+        chosen[j % T].append(e)
+    assert all(len(c) == K and len(set(c)) == K for c in chosen)
+    return T, chosen
+
+
+def _routing_columns(chosen, E, D, rng):
+    """x [T,D] whose first E columns fix the routing through a one-hot gate
+    Wg[e] = e_e (logit e = x[t,e], exact): the token's K experts get 2 + k/8,
+    the rest -1; the other columns are N(0,1)."""
+    T = len(chosen)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    x[:, :E] = -1.0
+    for t, es in enumerate(chosen):
+        for k, e in enumerate(es):
+            x[t, e] = 2.0 + 0.125 * k
+    wg = np.zeros((E, D), np.float32)
+    wg[np.arange(E), np.arange(E)] = 1.0
+    return x, wg
+
+
+def test_routed_layout_reaches_every_tile_count():
+    rs = {r for c in ROUTED_COUNTS for rows in _mtile_rows(c) for r in [-(-rows // 16)]}
+    assert rs == set(range(1, 17))
+    assert max(len(_mtile_rows(c)) for c in ROUTED_COUNTS) == 3
+
+
+def test_forward_fp8_every_token_tile_count(amd, orc, dsv3):
+    """DSV3 shape (E=256, K=8, D=7168, I=2048) with routing fixed through the
+    gate so that experts hold the row counts of ROUTED_COUNTS: every live
+    token-tile count R = 1..16 of the fp8 main loop, both register-ring
+    depths, two- and three-tile experts.  The full output of the row-major
+    and the packed entry is compared with the oracle (relative max error <=
+    2e-2 on the same dequantised fp8 values), and the two entries must agree
+    bit for bit."""
+    import synth
+    E, K, D, I = 256, 8, 7168, 2048
+    T, chosen = _routed_layout(ROUTED_COUNTS, E, K)
+    announce(f"forward_fp8 every token-tile count: T={T}, {len(ROUTED_COUNTS)} sized experts")
+    x, wg = _routing_columns(chosen, E, D, np.random.default_rng(1240))
+    xb, wgb = orc.f32_to_bf16(x), orc.f32_to_bf16(wg)
+    w1q, w1s, w2q, w2s = dsv3
+    cfg = amd.moe_config(T, E, K, D, I)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    amd.moe_forward_fp8(dev(xb), dev(wgb), w1q, w1s, w2q, w2s, y, cfg)
+    p1, p2 = _packed_pair(w1q, w2q)
+    yp = torch.empty_like(y)
+    amd.moe_forward_fp8_packed(dev(xb), dev(wgb), p1, w1s, p2, w2s, yp, cfg)
+    # the GPU's own routing and permutation: the counts asked for
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16(dev(xb), dev(wgb), idx, wts, cfg)
+    torch.cuda.synchronize()
+    del p1, p2
+    gi = host(idx)
+    assert [set(r) for r in gi.tolist()] == [set(c) for c in chosen]
+    counts = np.bincount(gi.reshape(-1), minlength=E)
+    assert counts[:len(ROUTED_COUNTS)].tolist() == ROUTED_COUNTS
+    assert torch.equal(y, yp)
+    used = np.unique(gi)
+    wmap = np.zeros(E, np.int32)
+    wmap[used] = np.arange(len(used), dtype=np.int32)
+    sel = torch.from_numpy(used).cuda()
+    q1 = w1q.index_select(0, sel).cpu().numpy(); s1 = w1s.index_select(0, sel).cpu().numpy()
+    q2 = w2q.index_select(0, sel).cpu().numpy(); s2 = w2s.index_select(0, sel).cpu().numpy()
+    idx_r, _, y_ref = orc.moe_forward_fp8(xb, wgb, q1, s1, q2, s2, K, wmap=wmap)
+    np.testing.assert_array_equal(np.sort(idx_r, 1), np.sort(gi, 1))
+    yg = orc.bf16_to_f32(bf16_np(y))
+    rel = np.abs(yg - y_ref).max() / np.abs(y_ref).max()
+    # per expert row count: the worst token among those the expert serves
+    tok_err = np.abs(yg - y_ref).max(1) / np.abs(y_ref).max()
+    worst = {c: float(tok_err[np.flatnonzero((gi == e).any(1))].max())
+             for e, c in enumerate(ROUTED_COUNTS)}
+    print(f"every tile count: rel_err={rel:.3e}; worst per count: "
+          + ", ".join(f"{c}:{v:.1e}" for c, v in worst.items()))
+    assert rel < 2e-2
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_forward_every_tile_group_f32_bf16(amd, orc, dtype):
+    """fp32 and bf16 main loops are instantiated per group of four 16-row
+    tiles (4, 8, 12, 16): routing fixed through the gate gives experts every
+    row count of ROUTED_COUNTS (all four groups, split experts); full output
+    against the oracle at the fp32 / bf16 bars."""
+    T, chosen = _routed_layout(ROUTED_COUNTS, 64, 2)
+    E, K, D, I = 64, 2, 128, 256
+    announce(f"forward_{dtype} every tile group: T={T}")
+    rng = np.random.default_rng(1250)
+    x, wg = _routing_columns(chosen, E, D, rng)
+    w1 = (rng.standard_normal((E, 2 * I, D)) / np.sqrt(D)).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, I)) / np.sqrt(I)).astype(np.float32)
+    cfg = amd.moe_config(T, E, K, D, I)
+    if dtype == "f32":
+        y = torch.empty((T, D), dtype=torch.float32, device="cuda")
+        amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), y, cfg)
+        torch.cuda.synchronize()
+        idx_r, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
+        err = np.abs(host(y) - y_ref).max()
+        bar = 1e-5 * max(1.0, np.abs(y_ref).max())
+    else:
+        xb, w1b, w2b = orc.f32_to_bf16(x), orc.f32_to_bf16(w1), orc.f32_to_bf16(w2)
+        y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+        amd.moe_forward_bf16(dev(xb), dev(wg), None, dev(w1b), dev(w2b), y, cfg)
+        torch.cuda.synchronize()
+        idx_r, _, y_ref = orc.moe_forward_bf16(xb, wg, w1b, w2b, K)
+        err = np.abs(orc.bf16_to_f32(bf16_np(y)) - y_ref).max()
+        bar = 2.0 ** -7 * np.abs(y_ref).max()
+    counts = np.bincount(idx_r.reshape(-1), minlength=E)
+    assert counts[:len(ROUTED_COUNTS)].tolist() == ROUTED_COUNTS
+    print(f"{dtype} every tile group: max_err={err:.3e} bar={bar:.3e}")
+    assert err < bar
+
+
+def test_forward_fp8_dsv3_t4096_tile_edges(amd, orc, dsv3):
+    """T=4096 on the GPU; the oracle checks 256 tokens: the first and the last
+    sorted row of 128 M-tiles (taken from the GPU's own routing and
+    permutation), where a tile's row bounds and masks act."""
+    import synth
+    T, E, K, D, I = 4096, 256, 8, 7168, 2048
+    announce("forward_fp8 dsv3 T=4096, 256 tile-edge tokens")
+    x, wg = synth.dsv3_inputs(T, E, D, seed=1235)
+    cfg = amd.moe_config(T, E, K, D, I)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16(x, wg, idx, wts, cfg)
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    st = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    ss = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    amd.moe_permute(idx, cfg, counts, offsets, st, ss)
+    torch.cuda.synchronize()
+    cn, of, stn = host(counts), host(offsets), host(st)
+    edges = []
+    for e in range(E):
+        first = int(of[e])
+        for rows in _mtile_rows(int(cn[e])):
+            edges += [int(stn[first]), int(stn[first + rows - 1])]
+            first += rows
+    rng = np.random.default_rng(4)
+    rows = np.unique(np.array(edges))
+    rows = np.sort(rng.choice(rows, min(256, len(rows)), replace=False))
+    assert len(rows) >= 200
+    assert _fp8_case(amd, orc, dsv3, T, E, K, D, I, sample=rows) < 2e-2
+
+
+def test_forward_bf16_mixtral_t256(amd, orc):
+    """BASELINE Mixtral config at T=256, every token checked."""
+    announce("forward_bf16 mixtral T=256")
+    err, _ = _bf16_case(amd, orc, 256, 8, 2, 4096, 14336, bias=False)
+    assert err < 1e-2
+
+
+def test_forward_f32_medium_with_bias(amd, orc):
+    """BASELINE medium config in fp32 (T=512, E=8, K=2, D=1024, I=2048,
+    N(0, 1/fan_in) weights) with the per-expert logit bias ~ N(0, 0.5^2) that
+    skews the expert loads, through amdmoe_moe_forward_f32_bias: indices as
+    the oracle's and the output within 1e-5 of max |y| (and the reference's
+    1e-3)."""
+    T, E, K, D, I = 512, 8, 2, 1024, 2048
+    announce("forward_f32 medium with bias")
+    rng = np.random.default_rng(512)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    wg = (rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    w1 = (rng.standard_normal((E, 2 * I, D)) / np.sqrt(D)).astype(np.float32)
+    w2 = (rng.standard_normal((E, D, I)) / np.sqrt(I)).astype(np.float32)
+    idx_r, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K, bias=b)
+    counts = np.bincount(idx_r.reshape(-1), minlength=E)
+    print(f"medium f32 expert loads: {counts.tolist()}")
+    y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    amd.moe_forward_f32_bias(dev(x), dev(wg), dev(b), dev(w1), dev(w2), y, amd.moe_config(T, E, K, D, I))
+    torch.cuda.synchronize()
+    err = np.abs(host(y) - y_ref).max()
+    print(f"medium f32 with bias: max_err={err:.3e} max|y|={np.abs(y_ref).max():.3f}")
+    assert err < 1e-3
+    assert err < 1e-5 * max(1.0, np.abs(y_ref).max())
+
+
+@pytest.mark.parametrize("T,E,K,D,I", [(37, 5, 3, 100, 50), (16, 4, 2, 33, 17), (300, 3, 2, 48, 40),
+                                       (9, 2, 2, 1, 1)])
+def test_forward_f32_any_shape(amd, orc, T, E, K, D, I):
+    """D and I that are not multiples of 32 (the reference takes any shape):
+    routing, gather and the whole forward against the oracle at the fp32
+    bar, on the reference's input distribution."""
+    announce(f"forward_f32 any shape {(T, E, K, D, I)}")
+    x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
+    idx_r, wts_r, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y = torch.full((T, D), float("nan"), dtype=torch.float32, device="cuda")
+    amd.moe_forward_f32(dev(x), dev(wg), dev(w1), dev(w2), y, cfg)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_f32(dev(x), dev(wg), idx, wts, cfg)
+    g = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    tmap = torch.full((T,), -1, dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    amd.moe_gather_f32(dev(x), idx, wts, E - 1, g, tmap, cnt, cfg)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_r)
+    toks = [t for t in range(T) if E - 1 in idx_r[t]]
+    assert int(cnt.item()) == len(toks)
+    np.testing.assert_array_equal(host(g)[:len(toks)], x[toks])
+    err = np.abs(host(y) - y_ref).max()
+    print(f"any shape {(T, E, K, D, I)}: max_err={err:.3e}")
+    assert err < 1e-3
+    assert err < 1e-5 * max(1.0, np.abs(y_ref).max())

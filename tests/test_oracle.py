@@ -377,6 +377,58 @@ def test_dsa_paged_equals_flat(orc):
     np.testing.assert_array_equal(out, ref)
 
 
+def test_dsa_paged_invalid_positions_select_nothing(orc):
+    """Selected positions that select nothing (-1 padding, an index past the
+    page-table row, a page id of -1 or past the cache) are left out: the
+    decode equals the reference restatement (dsa_forward_f32) run on the
+    flat rows of the valid positions only, and a query with none gives 0."""
+    rng = np.random.default_rng(11)
+    Q, H, Dc, Dp, S, page, pps = 3, 4, 64, 16, 24, 8, 6
+    n_pages = Q * pps
+    cache = orc.f32_to_bf16(rng.standard_normal((n_pages * page, Dc + Dp)).astype(np.float32))
+    pt = rng.permutation(n_pages).astype(np.int32).reshape(Q, pps)
+    pt[0, 2] = -1                 # an unmapped page
+    pt[0, 4] = n_pages + 5        # a page past the cache
+    logical = np.stack([rng.permutation(pps * page)[:S] for _ in range(Q)]).astype(np.int32)
+    logical[0, -5:] = -1          # padding
+    logical[0, 3] = pps * page    # past the row's capacity
+    logical[0, 4] = pps * page + 100
+    logical[2, :] = -1            # nothing valid
+    qn = orc.f32_to_bf16(rng.standard_normal((Q, H, Dc)).astype(np.float32))
+    qp = orc.f32_to_bf16(rng.standard_normal((Q, H, Dp)).astype(np.float32))
+    phys = orc.dsa_translate(logical, pt, page, cache_rows=n_pages * page)
+    # closed form: -1 exactly where the index, the page id or the row is out of range
+    ok = (logical >= 0) & (logical < pps * page)
+    pg = np.where(ok, pt[np.arange(Q)[:, None], np.clip(logical, 0, pps * page - 1) // page], -1)
+    row = pg * page + np.where(ok, logical % page, 0)
+    ok &= (pg >= 0) & (row < n_pages * page)
+    np.testing.assert_array_equal(phys, np.where(ok, row, -1))
+    assert (phys[0] == -1).sum() >= 7 and (phys[1] >= 0).all()
+    out = orc.dsa_decode_bf16_paged(qn, qp, cache, pt, logical, Dc, page)
+    cf = orc.bf16_to_f32(cache)
+    qnf, qpf = orc.bf16_to_f32(qn), orc.bf16_to_f32(qp)
+    for q in range(2):
+        rows = phys[q][phys[q] >= 0][None, :].astype(np.int32)
+        ref = orc.dsa_forward_f32(qnf[q:q + 1], qpf[q:q + 1], cf[:, :Dc].copy(), cf[:, Dc:].copy(),
+                                  cf[:, :Dc].copy(), rows)
+        np.testing.assert_array_equal(out[q], ref[0])
+    assert (out[2] == 0).all()
+
+
+def test_indexer_topk_capacity(orc):
+    """A row scores only min(seq_len, cap) positions: with fewer than top-k of
+    them the rest is -1 padding, never a position past the capacity."""
+    rng = np.random.default_rng(3)
+    sc = rng.standard_normal((2, 64)).astype(np.float32)
+    sc[:, 20:] = -np.inf
+    sl = np.array([64, 10], np.int32)
+    out = orc.dsa_indexer_topk(sc, sl, 32, cap=20)
+    np.testing.assert_array_equal(out[0], np.concatenate([np.arange(20), -np.ones(12, int)]))
+    np.testing.assert_array_equal(out[1], np.concatenate([np.arange(10), -np.ones(22, int)]))
+    out = orc.dsa_indexer_topk(sc, np.array([-4, 0], np.int32), 8)
+    assert (out == -1).all()
+
+
 @pytest.mark.parametrize("name,shape,tol", DSA_CASES, ids=[c[0] for c in DSA_CASES])
 def test_reference_dsa_cases_match_float64(orc, name, shape, tol):
     Q, H, Dc, Dp, S, P, N = shape
