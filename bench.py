@@ -61,13 +61,62 @@ def cpu_baseline(x, wg, w1q, w1s, w2q, w2s, K, n_tokens):
     q1, s1 = w1q.index_select(0, sel).cpu().numpy(), w1s.index_select(0, sel).cpu().numpy()
     q2, s2 = w2q.index_select(0, sel).cpu().numpy(), w2s.index_select(0, sel).cpu().numpy()
     oracle.lib()
+    threads = oracle.get_threads()
     t0 = time.perf_counter()
     oracle.moe_forward_fp8(xs, wgn, q1, s1, q2, s2, K, wmap=wmap)
     dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    del q1, s1, q2, s2
     return {"value": len(rows) / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{len(rows)} tokens of the T=4096 DSV3 fp8 workload (routing, x/act "
-                      f"quantisation, {len(used)} experts dequantised, combine); {dt:.1f} s"}
+                      f"quantisation, {len(used)} experts dequantised, combine); {dt:.1f} s",
+            "cpu_model": cpu_model(),
+            "single_core": cpu_single_core(K, x.shape[1], w2q.shape[2])}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_single_core(K, D, I, n_tokens=16):
+    """The faithful restatement of the reference's CPU oracle
+    (tests/test_moe.cu:32-140: fp32 weights, sequential sums) on ONE core,
+    at the DSV3 per-token shape: each token runs K expert FFNs of D x I
+    (a K-expert layer, E = K, so every token uses every expert: the
+    per-token work 6*K*D*I of the DSV3 layer; only the gate, E*D per token,
+    is smaller).  Timed on n_tokens tokens; the T=4096 time is that
+    extrapolated linearly in T (the oracle's cost is linear in T*K)."""
+    import numpy as np
+    import torch
+
+    import oracle
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    E = K
+    x = torch.randn((n_tokens, D), generator=g, device="cuda").cpu().numpy()
+    wg = (torch.randn((E, D), generator=g, device="cuda") / D ** 0.5).cpu().numpy()
+    w1 = (torch.randn((E, 2 * I, D), generator=g, device="cuda") / D ** 0.5).cpu().numpy()
+    w2 = (torch.randn((E, D, I), generator=g, device="cuda") / I ** 0.5).cpu().numpy()
+    prev = oracle.get_threads()
+    oracle.set_threads(1)
+    try:
+        t0 = time.perf_counter()
+        oracle.moe_forward_f32(x, wg, w1, w2, K)
+        dt = time.perf_counter() - t0
+    finally:
+        oracle.set_threads(prev)
+    del w1, w2
+    tps = n_tokens / dt
+    return {"value": round(tps, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "t4096_s_extrapolated": round(4096 / tps, 1),
+            "sample": f"{n_tokens} tokens, fp32 restatement of cpu_moe_forward on one core, "
+                      f"K={K} experts of D={D}, I={I} per token (DSV3 per-token work); "
+                      f"{dt:.1f} s; T=4096 extrapolated linearly"}
 
 
 def dsa_bench(amdmoe, synth, iters=20):

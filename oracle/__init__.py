@@ -36,6 +36,8 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         sig = {
             "orc_srand": (None, [ctypes.c_uint]),
+            "orc_set_threads": (None, [_I]),
+            "orc_get_threads": (_I, []),
             "orc_random_fill": (None, [_f32p, _L, _F, _F]),
             "orc_gen_sparse_indices": (None, [_i32p, _I, _I, _I, _I]),
             "orc_max_abs_error": (_F, [_f32p, _f32p, _L]),
@@ -89,6 +91,15 @@ def _opt(a):
     if a is None:
         return None
     return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def set_threads(n):
+    """Threads of the oracle's parallel loops (1 = the reference's single thread)."""
+    lib().orc_set_threads(int(n))
+
+
+def get_threads():
+    return int(lib().orc_get_threads())
 
 
 # ---------------------------------------------------------------- generators

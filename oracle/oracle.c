@@ -46,12 +46,19 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <omp.h>
 
 #define EXPORT __attribute__((visibility("default")))
 
 /* ------------------------------------------------------------------ */
 /* generators (glibc rand(): same expression as the reference)         */
 /* ------------------------------------------------------------------ */
+
+/* Threads of the oracle's parallel loops (the reference's CPU oracle is
+ * single-threaded; 1 reproduces it, more only split independent rows or
+ * output columns, so results are identical for any count). */
+EXPORT void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+EXPORT int orc_get_threads(void) { return omp_get_max_threads(); }
 
 /* utils/cuda_utils.cuh:56-60 */
 EXPORT void orc_srand(unsigned seed) { srand(seed); }
