@@ -130,6 +130,25 @@ int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight
                                   const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* Bytes of device scratch amdmoe_moe_forward_fp8_packed_noalloc owns per GPU. */
+#define AMDMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* amdmoe_moe_forward_fp8_packed for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and results as
+ * amdmoe_moe_forward_fp8_packed without the workspace: the scratch is a
+ * fixed AMDMOE_NOALLOC_SCRATCH_BYTES (64 MiB) device array inside the
+ * library, one per GPU, held until the process ends; the call allocates and
+ * frees nothing.  Configurations whose workspace (amdmoe_moe_workspace_bytes
+ * with AMDMOE_DTYPE_FP8) exceeds it are rejected with AMDMOE_ERR_WORKSPACE
+ * (at the DeepSeek-V3 shape, T up to about 400 tokens fit).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two host threads) race and must be ordered by the caller. */
+int amdmoe_moe_forward_fp8_packed_noalloc(const uint16_t* x, const uint16_t* gate_weight,
+                                          const uint8_t* w1_packed, const float* w1_scale,
+                                          const uint8_t* w2_packed, const float* w2_scale,
+                                          uint16_t* y, const MoeConfig* cfg, void* stream);
+
 /* One-time repacking of row-major expert weights [num_experts][rows][cols]
  * (bytes; W1 [E,2I,D] or W2 [E,D,I] e4m3, naive_moe.cuh:66-72) into
  * fragment-block order: per expert, per 16 rows x 128 bytes, 2 KB stored as

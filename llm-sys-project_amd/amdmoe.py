@@ -18,7 +18,8 @@ AMDMOE_DTYPE_FP8 = 2
 SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
     "amdmoe_moe_forward_f32", "amdmoe_moe_forward_f32_bias", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
-    "amdmoe_moe_forward_fp8_packed", "amdmoe_pack_weights_fp8",
+    "amdmoe_moe_forward_fp8_packed", "amdmoe_moe_forward_fp8_packed_noalloc",
+    "amdmoe_pack_weights_fp8",
     "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16", "amdmoe_moe_gate_fp8",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
@@ -73,6 +74,7 @@ def load():
         "amdmoe_moe_forward_bf16": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8_packed": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_moe_forward_fp8_packed_noalloc": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_pack_weights_fp8": (I, [_P, I, I, I, _P, _P]),
         "amdmoe_moe_gate_f32": (I, [_P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16x": (I, [_P, _P, _P, _P, _P, cfgp, _P]),
@@ -179,6 +181,17 @@ def moe_forward_fp8_packed(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=None, stream=No
     _check(load().amdmoe_moe_forward_fp8_packed(_ptr(x), _ptr(wg), _ptr(w1p), _ptr(w1s), _ptr(w2p),
                                                 _ptr(w2s), _ptr(y), ctypes.byref(cfg), p, n,
                                                 _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def moe_forward_fp8_packed_noalloc(x, wg, w1p, w1s, w2p, w2s, y, cfg, stream=None):
+    """amdmoe_moe_forward_fp8_packed with the library's fixed per-GPU scratch
+    (no allocation; workspace at most NOALLOC_SCRATCH_BYTES)."""
+    _check(load().amdmoe_moe_forward_fp8_packed_noalloc(_ptr(x), _ptr(wg), _ptr(w1p), _ptr(w1s),
+                                                        _ptr(w2p), _ptr(w2s), _ptr(y),
+                                                        ctypes.byref(cfg), _stream(stream)))
 
 
 def pack_weights_fp8(w, out, stream=None):

@@ -363,6 +363,32 @@ int amdmoe_moe_forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const
                        workspace_bytes, stream, false);
 }
 
+// ---------------------------------------------------------------- no allocation
+// Scratch of amdmoe_moe_forward_fp8_packed_noalloc: a file-scope device
+// array, one copy per GPU, held until the process ends.  In host code
+// `scratch` names a host-side stand-in, not device memory: its device
+// address is taken once per device with hipGetSymbolAddress (the entry's
+// first call on that device, with the device current) and only that address
+// is ever passed to a kernel.
+static __device__ __align__(256) uint8_t scratch[AMDMOE_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mutex;
+static void* g_scratch_dev[64];  // device address of `scratch` per device id
+
+static int noalloc_scratch(void** out) {
+    int dev = 0;
+    AMDMOE_HIP_TRY(hipGetDevice(&dev));
+    AMDMOE_CHECK_ARG(dev >= 0 && dev < 64, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mutex);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        AMDMOE_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        AMDMOE_CHECK_ARG(p != nullptr, "no device address for the scratch array");
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return AMDMOE_OK;
+}
+
 int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight,
                                   const uint8_t* w1_packed, const float* w1_scale,
                                   const uint8_t* w2_packed, const float* w2_scale, uint16_t* y,
@@ -370,6 +396,25 @@ int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight
                                   void* stream) {
     return forward_fp8(x, gate_weight, w1_packed, w1_scale, w2_packed, w2_scale, y, cfg, workspace,
                        workspace_bytes, stream, true);
+}
+
+int amdmoe_moe_forward_fp8_packed_noalloc(const uint16_t* x, const uint16_t* gate_weight,
+                                          const uint8_t* w1_packed, const float* w1_scale,
+                                          const uint8_t* w2_packed, const float* w2_scale,
+                                          uint16_t* y, const MoeConfig* cfg, void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_FP8));
+    const size_t need = ws_layout(*cfg, AMDMOE_DTYPE_FP8, nullptr).total;
+    if (need > (size_t)AMDMOE_NOALLOC_SCRATCH_BYTES)
+        return set_error(AMDMOE_ERR_WORKSPACE,
+                         "moe_forward_fp8_packed_noalloc: T=%d E=%d K=%d D=%d I=%d needs %zu bytes "
+                         "of scratch, more than the %zu of the no-allocation buffer",
+                         cfg->num_tokens, cfg->num_experts, cfg->top_k, cfg->hidden_dim,
+                         cfg->intermediate_dim, need, (size_t)AMDMOE_NOALLOC_SCRATCH_BYTES);
+    if (cfg->num_tokens == 0) return AMDMOE_OK;
+    void* ws = nullptr;
+    TRY(noalloc_scratch(&ws));
+    return forward_fp8(x, gate_weight, w1_packed, w1_scale, w2_packed, w2_scale, y, cfg, ws,
+                       AMDMOE_NOALLOC_SCRATCH_BYTES, stream, true);
 }
 
 int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int cols, uint8_t* out,
