@@ -69,6 +69,7 @@ typedef struct DsaConfig {
 #define AMDMOE_DTYPE_F32 0      /* fp32 in/out, fp32 intermediates            */
 #define AMDMOE_DTYPE_BF16 1     /* bf16 x/W1/W2/y, fp32 gate, bf16 activation */
 #define AMDMOE_DTYPE_FP8 2      /* e4m3 block-scaled experts, bf16 x/gate/y   */
+#define AMDMOE_DTYPE_MXFP4 3    /* OCP MXFP4 experts, MXFP8 activations, bf16 x/gate/y */
 
 /* Message of the last failing call on this host thread ("" if none). */
 const char* amdmoe_last_error(void);
@@ -129,6 +130,48 @@ int amdmoe_moe_forward_fp8_packed(const uint16_t* x, const uint16_t* gate_weight
                                   const uint8_t* w2_packed, const float* w2_scale, uint16_t* y,
                                   const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/* The MoE layer with OCP MXFP4 expert weights (OCP Microscaling spec v1.0;
+ * no counterpart in the reference, whose layer is fp32 only -- the AMD
+ * analogue of its roadmap's NVFP4 experts): every 32 consecutive weights
+ * along K share one E8M0 scale 2^(E-127), elements are FP4 E2M1.  x bf16
+ * [T,D] is quantised in the forward to MXFP8 (E4M3, one E8M0 scale per 32
+ * columns), as is the SwiGLU output; the MFMA applies all block scales.
+ * Weights in the fragment order of amdmoe_pack_weights_mxfp4:
+ * w1_packed [E, 2I*D/2] bytes with w1_scale_packed [E, 2I*D/32],
+ * w2_packed [E, D*I/2] with w2_scale_packed [E, D*I/32].  gate_weight bf16
+ * [E,D]; routing as amdmoe_moe_forward_fp8; y bf16 [T,D] overwritten.
+ * D and I multiples of 128; workspace as amdmoe_moe_workspace_bytes with
+ * AMDMOE_DTYPE_MXFP4. */
+int amdmoe_moe_forward_mxfp4(const uint16_t* x, const uint16_t* gate_weight,
+                             const uint8_t* w1_packed, const uint8_t* w1_scale_packed,
+                             const uint8_t* w2_packed, const uint8_t* w2_scale_packed, uint16_t* y,
+                             const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* MXFP4 quantisation of fp32 rows w [rows, cols] (cols % 32 == 0): q
+ * [rows, cols/2] E2M1 codes, two per byte, even column in the low nibble;
+ * scale [rows, cols/32] E8M0 = floor(log2 max|block|) - 2 + 127 clamped to
+ * [0, 254] (0 for an all-zero block); q = RNE(w / 2^(scale-127)) saturated
+ * at 6.  No counterpart in the reference. */
+int amdmoe_quant_weight_mxfp4(const float* w, long rows, int cols, uint8_t* q, uint8_t* scale,
+                              void* stream);
+
+/* MXFP8 quantisation of bf16 rows x [rows, cols] (cols % 32 == 0): q
+ * [rows, cols] E4M3, scale [rows, cols/32] E8M0 = floor(log2 max|block|) - 8
+ * + 127 clamped to [0, 254].  No counterpart in the reference. */
+int amdmoe_quant_rows_mxfp8(const uint16_t* x, long rows, int cols, uint8_t* q, uint8_t* scale,
+                            void* stream);
+
+/* One-time repacking of row-major MXFP4 expert weights (q [E][rows][cols/2],
+ * scale [E][rows][cols/32], as amdmoe_quant_weight_mxfp4 writes them) into
+ * the forward's fragment order: per expert, per 16 rows x 128 columns, 1 KB
+ * of codes stored [lane l][16 B] with lane l = 16g + r holding row r,
+ * columns 32g .. 32g+31 of the block, and the 64 scales [lane l] = scale of
+ * (row r, columns 32g ..); blocks ordered [rows/16][cols/128].  rows % 16
+ * == 0, cols % 128 == 0; outputs must not alias inputs. */
+int amdmoe_pack_weights_mxfp4(const uint8_t* q, const uint8_t* scale, int num_experts, int rows,
+                              int cols, uint8_t* q_packed, uint8_t* scale_packed, void* stream);
 
 /* Bytes of device scratch amdmoe_moe_forward_fp8_packed_noalloc owns per GPU. */
 #define AMDMOE_NOALLOC_SCRATCH_BYTES (64u << 20)

@@ -13,12 +13,14 @@ LIB_PATH = os.path.join(_HERE, "libamdmoe.so")
 AMDMOE_DTYPE_F32 = 0
 AMDMOE_DTYPE_BF16 = 1
 AMDMOE_DTYPE_FP8 = 2
+AMDMOE_DTYPE_MXFP4 = 3
 
 # Exported symbols, in the order include/amdmoe.h declares them.
 SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
     "amdmoe_moe_forward_f32", "amdmoe_moe_forward_f32_bias", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
-    "amdmoe_moe_forward_fp8_packed", "amdmoe_moe_forward_fp8_packed_noalloc",
+    "amdmoe_moe_forward_fp8_packed", "amdmoe_moe_forward_mxfp4", "amdmoe_quant_weight_mxfp4",
+    "amdmoe_quant_rows_mxfp8", "amdmoe_pack_weights_mxfp4", "amdmoe_moe_forward_fp8_packed_noalloc",
     "amdmoe_pack_weights_fp8",
     "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16", "amdmoe_moe_gate_fp8",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
@@ -74,6 +76,10 @@ def load():
         "amdmoe_moe_forward_bf16": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8_packed": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_moe_forward_mxfp4": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_quant_weight_mxfp4": (I, [_P, L_, I, _P, _P, _P]),
+        "amdmoe_quant_rows_mxfp8": (I, [_P, L_, I, _P, _P, _P]),
+        "amdmoe_pack_weights_mxfp4": (I, [_P, _P, I, I, I, _P, _P, _P]),
         "amdmoe_moe_forward_fp8_packed_noalloc": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_pack_weights_fp8": (I, [_P, I, I, I, _P, _P]),
         "amdmoe_moe_gate_f32": (I, [_P, _P, _P, _P, cfgp, _P]),
@@ -181,6 +187,31 @@ def moe_forward_fp8_packed(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=None, stream=No
     _check(load().amdmoe_moe_forward_fp8_packed(_ptr(x), _ptr(wg), _ptr(w1p), _ptr(w1s), _ptr(w2p),
                                                 _ptr(w2s), _ptr(y), ctypes.byref(cfg), p, n,
                                                 _stream(stream)))
+
+
+def moe_forward_mxfp4(x, wg, w1p, w1sp, w2p, w2sp, y, cfg, ws=None, stream=None):
+    """MXFP4 experts (fragment order, pack_weights_mxfp4), MXFP8 activations."""
+    p, n = _ws(ws)
+    _check(load().amdmoe_moe_forward_mxfp4(_ptr(x), _ptr(wg), _ptr(w1p), _ptr(w1sp), _ptr(w2p),
+                                           _ptr(w2sp), _ptr(y), ctypes.byref(cfg), p, n,
+                                           _stream(stream)))
+
+
+def quant_weight_mxfp4(w, q, s, stream=None):
+    rows, cols = w.shape
+    _check(load().amdmoe_quant_weight_mxfp4(_ptr(w), rows, cols, _ptr(q), _ptr(s), _stream(stream)))
+
+
+def quant_rows_mxfp8(x, q, s, stream=None):
+    rows, cols = x.shape
+    _check(load().amdmoe_quant_rows_mxfp8(_ptr(x), rows, cols, _ptr(q), _ptr(s), _stream(stream)))
+
+
+def pack_weights_mxfp4(q, s, qp, sp, stream=None):
+    """q [E, rows, cols/2], s [E, rows, cols/32] (uint8) -> fragment order."""
+    E, rows, half = q.shape
+    _check(load().amdmoe_pack_weights_mxfp4(_ptr(q), _ptr(s), E, rows, 2 * half, _ptr(qp), _ptr(sp),
+                                            _stream(stream)))
 
 
 NOALLOC_SCRATCH_BYTES = 64 << 20

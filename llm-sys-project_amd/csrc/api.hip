@@ -55,6 +55,7 @@ struct MoeWs {
 };
 
 static int elem_size(int dtype) { return dtype == AMDMOE_DTYPE_F32 ? 4 : (dtype == AMDMOE_DTYPE_BF16 ? 2 : 1); }
+static bool is_8bit(int dtype) { return dtype == AMDMOE_DTYPE_FP8 || dtype == AMDMOE_DTYPE_MXFP4; }
 
 // Lays the workspace out from `base` (nullptr: sizes only).
 static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
@@ -78,13 +79,15 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     w.sorted_slot = (int*)take(4 * P);
     w.sorted_w = (float*)take(4 * P);
     w.perm = (int*)take(permute_scratch_bytes((int)T, (int)E));
-    if (dtype == AMDMOE_DTYPE_FP8) {
+    if (is_8bit(dtype)) {
+        // activation scales: fp8 one fp32 per 128 columns, MX one E8M0 byte
+        // per 32 -- the same bytes per row
         w.xq = take(T * D);
         w.xs = (float*)take(4 * T * (D / 128));
         w.act = take(P * I);
         w.act_s = (float*)take(4 * P * (I / 128));
         w.ypair = take(2 * P * D);
-        w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E, (int)D, true));
+        w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E, (int)D, dtype == AMDMOE_DTYPE_FP8));
     } else {
         const size_t es = elem_size(dtype);
         w.act = take(es * P * I);
@@ -137,7 +140,7 @@ static int check_cfg(const MoeConfig* cfg, int dtype) {
     AMDMOE_CHECK_ARG((long)c.num_tokens * c.top_k < (1L << 30), "T*K=%ld too large", (long)c.num_tokens * c.top_k);
     // fp32 (the reference's format) takes any D and I; the bf16 / fp8 tiles
     // need whole 64- / 128-element K steps (and the fp8 block scales 128)
-    const int kq = dtype == AMDMOE_DTYPE_F32 ? 1 : (dtype == AMDMOE_DTYPE_BF16 ? 64 : 128);
+    const int kq = dtype == AMDMOE_DTYPE_F32 ? 1 : (dtype == AMDMOE_DTYPE_BF16 ? 64 : 128);  // fp8, MXFP4: 128
     AMDMOE_CHECK_ARG(c.hidden_dim % kq == 0 && c.intermediate_dim % kq == 0,
                      "hidden_dim=%d and intermediate_dim=%d must be multiples of %d for this dtype",
                      c.hidden_dim, c.intermediate_dim, kq);
@@ -188,7 +191,8 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
               I = c.intermediate_dim;
     const long P = (long)T * K;
     const long mtiles = max_mtiles(P, E);
-    const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);
+    const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);  // activation bytes per element
+    const int wdiv = dt == DT_MX ? 2 : 1;                       // MX weights: two E2M1 per byte
     TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
                        w.sorted_slot, w.tiles, w.num_tiles,
                        permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st));
@@ -210,8 +214,10 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     up.a_scale = x_scale;
     up.a_scale_bytes = x_scale ? (long)T * (D / 128) * 4 : 0;
     up.b = w1;
-    up.b_expert_bytes = 2L * I * D * es;
-    up.b_row_bytes = (long)D * es;
+    up.b_expert_bytes = 2L * I * D * es / wdiv;
+    up.b_row_bytes = (long)D * es / wdiv;
+    up.b_mx_scale = dt == DT_MX ? (const uint8_t*)w1s : nullptr;
+    up.b_mx_scale_expert_bytes = dt == DT_MX ? 2L * I * (D / 32) : 0;
     up.b_packed = packed;
     up.b_scale = w1s;
     up.b_rows = 2 * I;
@@ -231,8 +237,10 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.a_scale = w.act_s;
     dn.a_scale_bytes = w.act_s ? P * (I / 128) * 4 : 0;
     dn.b = w2;
-    dn.b_expert_bytes = (long)D * I * es;
-    dn.b_row_bytes = (long)I * es;
+    dn.b_expert_bytes = (long)D * I * es / wdiv;
+    dn.b_row_bytes = (long)I * es / wdiv;
+    dn.b_mx_scale = dt == DT_MX ? (const uint8_t*)w2s : nullptr;
+    dn.b_mx_scale_expert_bytes = dt == DT_MX ? (long)D * (I / 32) : 0;
     dn.b_packed = packed;
     dn.b_scale = w2s;
     dn.b_rows = D;
@@ -266,7 +274,7 @@ int amdmoe_set_stage_events(void** events) {
 }
 
 int amdmoe_moe_workspace_bytes(const MoeConfig* cfg, int dtype, size_t* bytes) {
-    AMDMOE_CHECK_ARG(dtype >= AMDMOE_DTYPE_F32 && dtype <= AMDMOE_DTYPE_FP8, "bad dtype %d", dtype);
+    AMDMOE_CHECK_ARG(dtype >= AMDMOE_DTYPE_F32 && dtype <= AMDMOE_DTYPE_MXFP4, "bad dtype %d", dtype);
     TRY(check_cfg(cfg, dtype));
     AMDMOE_CHECK_ARG(bytes != nullptr, "bytes is NULL");
     *bytes = ws_layout(*cfg, dtype, nullptr).total;
@@ -415,6 +423,50 @@ int amdmoe_moe_forward_fp8_packed_noalloc(const uint16_t* x, const uint16_t* gat
     TRY(noalloc_scratch(&ws));
     return forward_fp8(x, gate_weight, w1_packed, w1_scale, w2_packed, w2_scale, y, cfg, ws,
                        AMDMOE_NOALLOC_SCRATCH_BYTES, stream, true);
+}
+
+int amdmoe_moe_forward_mxfp4(const uint16_t* x, const uint16_t* gate_weight,
+                             const uint8_t* w1_packed, const uint8_t* w1_scale_packed,
+                             const uint8_t* w2_packed, const uint8_t* w2_scale_packed, uint16_t* y,
+                             const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    TRY(check_cfg(cfg, AMDMOE_DTYPE_MXFP4));
+    const MoeConfig& c = *cfg;
+    if (c.num_tokens == 0) return AMDMOE_OK;
+    AMDMOE_CHECK_ARG(x && gate_weight && w1_packed && w1_scale_packed && w2_packed && w2_scale_packed && y,
+                     "null tensor pointer");
+    hipStream_t st = (hipStream_t)stream;
+    MoeWs w;
+    TRY(resolve_ws(c, AMDMOE_DTYPE_MXFP4, workspace, workspace_bytes, &w));
+    TRY(mark(0, st));
+    if (route_mfma_supported(c.num_experts, c.top_k, c.hidden_dim))
+        TRY(launch_route_mfma(x, gate_weight, c.num_tokens, c.num_experts, c.top_k, c.hidden_dim,
+                              w.idx, w.wts, w.logits, nullptr, nullptr, st));
+    else
+        TRY(launch_route_exact<uint16_t, uint16_t>(x, gate_weight, nullptr, c.num_tokens,
+                                                   c.num_experts, c.top_k, c.hidden_dim, w.idx,
+                                                   w.wts, st));
+    TRY(mark(1, st));
+    TRY(launch_quant_rows_mxfp8(x, c.num_tokens, c.hidden_dim, w.xq, (uint8_t*)w.xs, st));
+    TRY(mark(2, st));
+    return moe_experts(DT_MX, c, w, w.xq, w.xs, w1_packed, (const float*)w1_scale_packed, w2_packed,
+                       (const float*)w2_scale_packed, y, st, true);
+}
+
+int amdmoe_quant_weight_mxfp4(const float* w, long rows, int cols, uint8_t* q, uint8_t* scale,
+                              void* stream) {
+    return launch_quant_weight_mxfp4(w, rows, cols, q, scale, (hipStream_t)stream);
+}
+
+int amdmoe_quant_rows_mxfp8(const uint16_t* x, long rows, int cols, uint8_t* q, uint8_t* scale,
+                            void* stream) {
+    return launch_quant_rows_mxfp8(x, rows, cols, q, scale, (hipStream_t)stream);
+}
+
+int amdmoe_pack_weights_mxfp4(const uint8_t* q, const uint8_t* scale, int num_experts, int rows,
+                              int cols, uint8_t* q_packed, uint8_t* scale_packed, void* stream) {
+    return launch_pack_mxfp4(q, scale, num_experts, rows, cols, q_packed, scale_packed,
+                             (hipStream_t)stream);
 }
 
 int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int cols, uint8_t* out,

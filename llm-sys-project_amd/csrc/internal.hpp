@@ -6,7 +6,7 @@
 
 namespace amdmoe {
 
-enum { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2 };
+enum { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_MX = 3 };  // DT_MX: MXFP4 weights x MXFP8 activations
 enum { MODE_UP = 0, MODE_DOWN = 1 };
 
 constexpr int kMTile = 256;  // rows of one grouped-GEMM M-tile
@@ -33,6 +33,10 @@ struct GemmArgs {
     float* out_scale;        // UP fp8: act scales [P, I/128]
     const int* sorted_slot;  // DOWN: flat slot t*K+k of each sorted row
     const float* sorted_w;   // DOWN: routing weight of each sorted row
+    // MX only: E8M0 weight scales in fragment order [E][b_rows/16][K/128][64]
+    // (a_scale then holds the activations' E8M0 scales, [A rows][K/32] bytes)
+    const uint8_t* b_mx_scale;
+    long b_mx_scale_expert_bytes;
 };
 
 // moe_route.hip
@@ -74,6 +78,14 @@ int launch_experts_f32_any(const float* x, const float* w1, const float* w2, int
                            int D, int I, const int4* tiles, const int* num_tiles, long max_tiles,
                            const int* sorted_token, const int* sorted_slot, const float* sorted_w,
                            const int* idx, float* act, float* ypair, float* y, hipStream_t st);
+
+// moe_mx.hip: OCP MX quantisers and the MXFP4 weight packer
+int launch_quant_weight_mxfp4(const float* w, long rows, int cols, uint8_t* q, uint8_t* s,
+                              hipStream_t st);
+int launch_quant_rows_mxfp8(const uint16_t* x, long rows, int cols, uint8_t* q, uint8_t* s,
+                            hipStream_t st);
+int launch_pack_mxfp4(const uint8_t* q, const uint8_t* s, long E, int N, int K, uint8_t* qp,
+                      uint8_t* sp, hipStream_t st);
 
 // moe_pack.hip: [E][N][K]-byte weights -> fragment-block order (N % 16 == 0,
 // K % 128 == 0)

@@ -62,6 +62,9 @@ constexpr int kSTile = 8 * 256;                        // A-scale slots, 256 B p
 constexpr int kStageBytes = kATile + kSTile;           // 34816
 constexpr int kBScaleOff = kNS * kStageBytes;          // fp8 weight scales [2][kMaxKb]
 constexpr int kMaxKb = 128;                            // K <= 16384 on the fp8 path
+// weight register sets of the main loop's ring (RB - 1 K-steps of weights in
+// flight) for up to 12 live token tiles and for more
+constexpr int kRbSmall = 4, kRbLarge = 3;
 constexpr int kEpiPitch = 132;                         // floats per staged output row
 constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
 constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
@@ -74,6 +77,7 @@ template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
 template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
 template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
+template <> struct DtTraits<DT_MX> { static constexpr int es = 1; };  // activation bytes per element
 
 // One K-step of a wave's weights in registers: per column tile the lane's
 // 32 bytes, lo 16 B at K offset 16q and hi 16 B at 64 + 16q (the fp8 MFMA
@@ -82,10 +86,20 @@ struct BFrag {
     u32x4 q[2][2];  // [column tile][lo, hi]
 };
 
+// MXFP4: per column tile the lane's 16 bytes of E2M1 weights (32 elements,
+// one E8M0 block) and that block's scale byte.
+struct BFragMx {
+    u32x4 w[2];
+    uint32_t s[2];
+};
+
 // An empty asm that reads and redefines the fragment: no use of it can move
 // above this point, and the compiler must assume its value changes here.
 __device__ __forceinline__ void pin(BFrag& f) {
     asm volatile("" : "+v"(f.q[0][0]), "+v"(f.q[0][1]), "+v"(f.q[1][0]), "+v"(f.q[1][1]));
+}
+__device__ __forceinline__ void pin(BFragMx& f) {
+    asm volatile("" : "+v"(f.w[0]), "+v"(f.w[1]), "+v"(f.s[0]), "+v"(f.s[1]));
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -112,6 +126,25 @@ __device__ __forceinline__ u32x4 buffer_load_b128_async(i32x4 rsrc, uint32_t vof
     return r;
 }
 
+// One byte, zero-extended (the MX weight scale of the lane's block), as
+// asm for the same reason.
+__device__ __forceinline__ uint32_t buffer_load_u8_async(i32x4 rsrc, uint32_t voff, int soff) {
+    uint32_t r;
+    asm volatile("buffer_load_ubyte %0, %1, %2, %3 offen"
+                 : "=v"(r)
+                 : "v"(voff), "s"(rsrc), "s"(soff));
+    return r;
+}
+
+// 16x16x128 MFMA, A = MXFP4 weights (E2M1, 4 registers used), B = MXFP8
+// activations, with the hardware applying each operand's E8M0 block scale
+// (byte 0 of sa / sb): scale j belongs to K elements 32j..32j+31 of the
+// step for both operands (the lanes of group j supply it).
+__device__ __forceinline__ f32x4 mfma_mx(const u32x4& w, const i32x8& x, uint32_t sa, uint32_t sb, f32x4 c) {
+    const i32x8 a = {(int)w[0], (int)w[1], (int)w[2], (int)w[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, x, c, 4, 0, 0, (int)sa, 0, (int)sb);
+}
+
 __device__ __forceinline__ i32x8 frag8(const BFrag& f, int ct) {
     const u32x4 a = f.q[ct][0], b = f.q[ct][1];
     return (i32x8){(int)a[0], (int)a[1], (int)a[2], (int)a[3], (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
@@ -131,10 +164,14 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int ES = DtTraits<DT>::es;
     // vector-memory instructions per K-step per wave ("slots"): 4
-    // activation slabs (+1 scale slot on fp8) into LDS, then 4 weight loads
-    // into registers; a wave whose activation rows are all past the live
-    // token tiles issues only the weight loads
-    constexpr int kASlots = 4 + (DT == DT_FP8 ? 1 : 0);
+    // activation slabs (+1 scale slot on fp8 / MX) into LDS, then 4 weight
+    // loads into registers (MX: per column tile 16 bytes of E2M1 and one
+    // scale byte); a wave whose activation rows are all past the live token
+    // tiles issues only the weight loads
+    constexpr bool kScaledA = DT == DT_FP8 || DT == DT_MX;  // activations carry row scales
+    static_assert(DT != DT_MX || PK, "MX weights exist in fragment order only");
+    using Frag = std::conditional_t<DT == DT_MX, BFragMx, BFrag>;
+    constexpr int kASlots = 4 + (kScaledA ? 1 : 0);
     constexpr int kSlots = kASlots + 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -157,8 +194,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
     const i32x4 rb = make_rsrc_words(bexp, g.b_expert_bytes);
     const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(DT == DT_FP8 ? (const void*)g.a_scale : (const void*)g.a,
-                  DT == DT_FP8 ? g.a_scale_bytes : 0);
+        make_rsrc(kScaledA ? (const void*)g.a_scale : (const void*)g.a,
+                  kScaledA ? g.a_scale_bytes : 0);
+    const i32x4 rbs = DT == DT_MX ? make_rsrc_words(g.b_mx_scale + (size_t)e * g.b_mx_scale_expert_bytes,
+                                                    g.b_mx_scale_expert_bytes)
+                                  : rb;
 
     // ---- activation DMA offsets: wave w fills rows [32w, 32w+32) ----
     const int lrow = lane >> 3;              // row within an 8-row, 1 KB slab
@@ -196,8 +236,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         const int r = 32 * wave + 8 * j + lrow;
         voff_a[j] = r < rows ? (uint32_t)(arow[j] * g.a_row_bytes + 16 * lchunk) : kOob;
     }
+    // activation scales of a K-step: fp8 one fp32 per row, MX the row's four
+    // E8M0 bytes -- both one dword per row and step, [rows][K/128] dwords
     uint32_t voff_s = kOob;
-    if (DT == DT_FP8) {
+    if (kScaledA) {
         const int r = 32 * wave + lane;
         if (lane < 32 && r < rows) voff_s = (uint32_t)(arow[4] * kb_per_row * 4);
     }
@@ -206,7 +248,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     //   UP:   ct 0 = gate rows n0 + 16w + c, ct 1 = up rows I + n0 + 16w + c
     //   DOWN: ct = rows n0 + 32w + 16ct + c
     const int q = lane >> 4, r16 = lane & 15;
-    uint32_t voff_b[2];
+    uint32_t voff_b[2], voff_bs[2];
     for (int ct = 0; ct < 2; ct++) {
         long n;
         bool ok;
@@ -223,6 +265,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // [half][lane][16 B], so each load is 1 KB contiguous
         const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
         voff_b[ct] = ok ? (uint32_t)nb : kOob;
+        // MX: E8M0 scales of the 16 rows' K-step, [lane] bytes per block of 64
+        voff_bs[ct] = ok ? (uint32_t)((n - r16) / 16 * nk * 64 + lane) : kOob;
     }
     __builtin_amdgcn_sched_barrier(0);
     int row_slot = 0;
@@ -255,7 +299,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // K-step kt into ring stage st / register set f.
     // Activation slots load K-step kt_a into ring stage kt_a % kNS, weight
     // slots load K-step kt_b into the register set f.
-    auto issue_slot = [&](int sl, bool a_live, int kt_a, int kt_b, BFrag& f) __attribute__((always_inline)) {
+    auto issue_slot = [&](int sl, bool a_live, int kt_a, int kt_b, Frag& f) __attribute__((always_inline)) {
         if (sl < kASlots) {
             if (!a_live) return;
             const bool live = kt_a < nk;
@@ -273,10 +317,18 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const bool live = kt_b < nk;
             const int kb = kblk(kt_b);
             const int ct = (sl - kASlots) >> 1;
-            const uint32_t vo = live ? voff_b[ct] : kOob;
-            const int sstep = PK ? kb * 2048 : kb * 128;
-            if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (PK ? 1024 : 64));
-            else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
+            if constexpr (DT == DT_MX) {
+                // 1 KB of E2M1 (16 rows x 128 K) and the 64 scale bytes of the block
+                if ((sl - kASlots) & 1)
+                    f.s[ct] = buffer_load_u8_async(rbs, live ? voff_bs[ct] : kOob, kb * 64);
+                else
+                    f.w[ct] = buffer_load_b128_async<0>(rb, live ? voff_b[ct] : kOob, kb * 1024);
+            } else {
+                const uint32_t vo = live ? voff_b[ct] : kOob;
+                const int sstep = PK ? kb * 2048 : kb * 128;
+                if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (PK ? 1024 : 64));
+                else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
+            }
         }
     };
 
@@ -290,7 +342,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // C^T = W x^T: weights are operand A (rows = weight columns), tokens
     // operand B, so each lane owns a single token and the activation block
     // scale is one float per lane, while the weight block scale is uniform.
-    auto compute = [&](auto rc, const BFrag& bf, int kt, auto&& tile_issued) __attribute__((always_inline)) {
+    auto compute = [&](auto rc, const Frag& bf, int kt, auto&& tile_issued) __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;
         // the stage offset is made opaque so the compiler forms the LDS
         // addresses here (one add, then immediate offsets) rather than
@@ -310,14 +362,20 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const u32x4 lo = *(const u32x4*)(p + off_lo), hi = *(const u32x4*)(p + off_hi);
             xv = (i32x8){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-            if (DT == DT_FP8) {
+            if (kScaledA) {  // fp8: the row's fp32 scale; MX: its four E8M0 bytes
                 const int r = 16 * rt + r16;
                 sx = *(const float*)(base + kATile + (r >> 5) * 256 + (r & 31) * 4);
             }
         };
         auto mma = [&](int rt, const i32x8& xv, float sx) __attribute__((always_inline)) {
             const u32x4 xlo = lo4(xv), xhi = hi4(xv);
-            if (DT == DT_FP8) {
+            if constexpr (DT == DT_MX) {
+                // block scales applied by the MFMA: the weights' from the
+                // lane's scale byte, the token's from byte q of its dword
+                const uint32_t sbx = __float_as_uint(sx) >> (8 * q);
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) acc[rt][ct] = mfma_mx(bf.w[ct], xv, bf.s[ct], sbx, acc[rt][ct]);
+            } else if constexpr (DT == DT_FP8) {
                 const float s0 = sx * sb0;
                 const float s1 = MODE == MODE_UP ? sx * sb1 : s0;
 #pragma unroll
@@ -329,7 +387,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             } else {
 #pragma unroll
                 for (int ct = 0; ct < 2; ct++) {
-                    const u32x4 wlo = bf.q[ct][0], whi = bf.q[ct][1];
+                    const u32x4 wlo = bf.q[ct][0], whi = bf.q[ct][1];  // f32 / bf16
                     if (DT == DT_F32) {
                         for (int j = 0; j < 4; j++)
                             acc[rt][ct] = mfma_f32(__uint_as_float(wlo[j]), __uint_as_float(xlo[j]), acc[rt][ct]);
@@ -349,9 +407,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // the next tile's MFMAs are issued, so the VALU never waits on an
         // MFMA it just issued (products of two tiles live, 16 registers).
         auto mfma_pair = [&](const i32x8& xv, f32x4& p0, f32x4& p1) __attribute__((always_inline)) {
-            p0 = mfma_fp8(frag8(bf, 0), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
-            p1 = mfma_fp8(frag8(bf, 1), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
-            asm volatile("" : "+v"(p0), "+v"(p1));
+            if constexpr (DT == DT_FP8) {
+                p0 = mfma_fp8(frag8(bf, 0), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
+                p1 = mfma_fp8(frag8(bf, 1), xv, (f32x4){0.f, 0.f, 0.f, 0.f});
+                asm volatile("" : "+v"(p0), "+v"(p1));
+            }
         };
         auto fold = [&](int rt, const f32x4& p0, const f32x4& p1, float sx) __attribute__((always_inline)) {
             const float s0 = sx * sb0;
@@ -409,7 +469,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // step's loads at once parks every wave at the issue for most of the
     // step.  Slot s goes out right after the MFMAs of token tile
     // (s * tiles) / kSlots, so the activation slots go first.
-    auto step = [&](auto stc, auto rc, auto rbc, bool a_live, int kt, BFrag& cur, BFrag& refill)
+    auto step = [&](auto stc, auto rc, auto rbc, bool a_live, int kt, Frag& cur, Frag& refill)
                     __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;  // token tiles per step
         constexpr int RB = decltype(rbc)::value;
@@ -428,8 +488,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         //            4 + kASlots + 4 later instructions, this also waits for
         //            the first activation slot of step kt+1 (one count for
         //            all waves: no path mixes the two).
-        static_assert(RB == 5 || RB == 4 || RB == 3, "wait counts are derived for rings of 3, 4 or 5 sets");
-        wait_vmcnt<RB == 5 ? 12 : (RB == 4 ? 8 : 4)>();
+        //   RB == 2: the weights of step kt were the last loads issued, so
+        //            nothing may be outstanding (the activations of step
+        //            kt+1, issued before them, are waited for one step early).
+        static_assert(RB >= 2 && RB <= 5, "wait counts are derived for rings of 2 to 5 sets");
+        wait_vmcnt<RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0))>();
         // the weights of this step have landed: pin every use of them below
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
@@ -446,20 +509,21 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // sets are defined and consumed in one place with no moves between.
     auto main_loop = [&](auto rc) __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;
-        constexpr int RB = R <= 12 ? 4 : 3;
+        constexpr int RB = R <= 12 ? kRbSmall : kRbLarge;
         const std::integral_constant<int, RB> rbc;
         const bool a_live = 32 * wave < 16 * R;  // uniform
         // only the live token tiles' accumulators exist during the loop
 #pragma unroll
         for (int i = 0; i < R; i++)
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        BFrag bs[RB];
+        Frag bs[RB];
         // prologue, in the steady-state issue order: per step the
-        // activation slots (steps 0, 1) before the weight slots
-        static_for<RB - 1>([&](auto ic) __attribute__((always_inline)) {
+        // activation slots (steps 0, 1) before the weight slots (steps
+        // 0..RB-2)
+        static_for<(RB - 1 > 2 ? RB - 1 : 2)>([&](auto ic) __attribute__((always_inline)) {
             constexpr int i = decltype(ic)::value;
             for (int sl = 0; sl < kSlots; sl++)
-                if (sl >= kASlots || i < 2) issue_slot(sl, a_live, i, i, bs[i]);
+                if (sl < kASlots ? i < 2 : i < RB - 1) issue_slot(sl, a_live, i, i, bs[i < RB ? i : 0]);
         });
         for (int kt = 0; kt < nk; kt += RB) {
             static_for<RB>([&](auto stc) __attribute__((always_inline)) {
@@ -475,12 +539,12 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         for (int i = R; i < 16; i++)
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     };
-    // The loop is instantiated per live token-tile count: fp8 (the layer's
-    // headline path, where an expert's 128 +- 11 rows would otherwise be
-    // rounded up to 192) in steps of one 16-row tile, the fp32 / bf16 paths
-    // in groups of four.
+    // The loop is instantiated per live token-tile count: fp8 and MX (the
+    // layer's headline paths, where an expert's 128 +- 11 rows would
+    // otherwise be rounded up to 192) in steps of one 16-row tile, the fp32 /
+    // bf16 paths in groups of four.
     const int ntiles = (rows + 15) / 16;  // 1..16, uniform
-    if constexpr (DT == DT_FP8) {
+    if constexpr (kScaledA) {
         static_for<16>([&](auto ic) __attribute__((always_inline)) {
             constexpr int R = decltype(ic)::value + 1;
             if (ntiles == R) main_loop(std::integral_constant<int, R>());
@@ -552,6 +616,28 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     *(u32x4*)dst = o0;
                     *(u32x4*)(dst + 16) = o1;
                     if (pp == 0) g.out_scale[pos * (g.n_out / 128) + nt] = s;
+                }
+            } else if (DT == DT_MX) {
+                // MXFP8 (OCP MX): the thread's 32 columns are one block;
+                // E8M0 exponent = floor(log2 amax) - 8 (E4M3's largest
+                // binade), clamped to [0, 254]; codes = e4m3(v * 2^(127 - E)),
+                // an exact power-of-two scaling
+                float amax = 0.0f;
+                for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+                const int e8 = min(max((int)((__float_as_uint(amax) >> 23) & 0xff) - 8, 0), 254);
+                const float inv = __builtin_amdgcn_ldexpf(1.0f, 127 - e8);
+                if (ok) {
+                    u32x4 o0, o1;
+                    for (int k = 0; k < 4; k++) {
+                        o0[k] = f32x4_to_e4m3x4(v[4 * k] * inv, v[4 * k + 1] * inv,
+                                                v[4 * k + 2] * inv, v[4 * k + 3] * inv);
+                        o1[k] = f32x4_to_e4m3x4(v[16 + 4 * k] * inv, v[16 + 4 * k + 1] * inv,
+                                                v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
+                    }
+                    uint8_t* dst = g.out + pos * g.n_out + col;
+                    *(u32x4*)dst = o0;
+                    *(u32x4*)(dst + 16) = o1;
+                    ((uint8_t*)g.out_scale)[pos * (g.n_out / 32) + col / 32] = (uint8_t)e8;
                 }
             } else if (DT == DT_BF16) {
                 if (ok) {
@@ -662,6 +748,8 @@ AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, true)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, false)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, true)
+AMDMOE_GEMM_VARIANT(DT_MX, MODE_UP, true)
+AMDMOE_GEMM_VARIANT(DT_MX, MODE_DOWN, true)
 #undef AMDMOE_GEMM_VARIANT
 
 }  // namespace amdmoe

@@ -41,6 +41,35 @@ def dsv3_weights(E, D, I, seed=1234, device="cuda"):
     return w1q, w1s, w2q, w2s
 
 
+def mxfp4_weights(E, D, I, seed=1234, device="cuda", packed=True):
+    """MXFP4 expert weights of the DSV3 layer shape: W1 [E,2I,D], W2 [E,D,I]
+    ~ N(0, 1/fan_in) quantised by amdmoe_quant_weight_mxfp4 (E2M1, E8M0 per
+    32 along K), built one expert at a time; packed (fragment order,
+    amdmoe_pack_weights_mxfp4) unless packed=False, which returns the
+    row-major codes and scales."""
+    g = _gen(seed, device)
+    w1q = torch.empty((E, 2 * I, D // 2), dtype=torch.uint8, device=device)
+    w1s = torch.empty((E, 2 * I, D // 32), dtype=torch.uint8, device=device)
+    w2q = torch.empty((E, D, I // 2), dtype=torch.uint8, device=device)
+    w2s = torch.empty((E, D, I // 32), dtype=torch.uint8, device=device)
+    for e in range(E):
+        w = torch.randn((2 * I, D), generator=g, device=device) * (1.0 / D ** 0.5)
+        amdmoe.quant_weight_mxfp4(w, w1q[e], w1s[e])
+        w = torch.randn((D, I), generator=g, device=device) * (1.0 / I ** 0.5)
+        amdmoe.quant_weight_mxfp4(w, w2q[e], w2s[e])
+        del w
+    if not packed:
+        torch.cuda.synchronize()
+        return w1q, w1s, w2q, w2s
+    out = []
+    for q, s in ((w1q, w1s), (w2q, w2s)):
+        qp, sp = torch.empty_like(q), torch.empty_like(s)
+        amdmoe.pack_weights_mxfp4(q, s, qp, sp)
+        out += [qp, sp]
+    torch.cuda.synchronize()
+    return tuple(out)
+
+
 def dsv3_inputs(T, E, D, seed=99, device="cuda"):
     """x bf16 [T,D] ~ N(0,1) and gate bf16 [E,D] ~ N(0, 1/D), as int16 bit views."""
     g = _gen(seed, device)

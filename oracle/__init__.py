@@ -60,6 +60,13 @@ def lib():
             "orc_dequant_weight_128x128": (None, [_u8p, _f32p, _I, _I, _f32p]),
             "orc_moe_forward_fp8": (None, [_u16p, _I, _u16p, _u8p, _f32p, _u8p, _f32p,
                                            ctypes.c_void_p, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
+            "orc_e8m0_to_f32": (_F, [ctypes.c_uint8]),
+            "orc_e2m1_to_f32": (_F, [ctypes.c_uint8]),
+            "orc_f32_to_e2m1": (ctypes.c_uint8, [_F]),
+            "orc_mx_quant_rows": (None, [_f32p, _L, _I, _I, _u8p, _u8p]),
+            "orc_mx_dequant_rows": (None, [_u8p, _u8p, _L, _I, _I, _f32p]),
+            "orc_moe_forward_mxfp4": (None, [_u16p, _I, _u16p, _u8p, _u8p, _u8p, _u8p,
+                                             ctypes.c_void_p, _I, _I, _I, _I, _i32p, _f32p, _f32p]),
             "orc_dsa_kv_gather": (None, [_f32p, ctypes.c_void_p, _f32p, _i32p, _f32p,
                                          ctypes.c_void_p, _f32p, _I, _I, _I, _I]),
             "orc_dsa_dot": (None, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -279,6 +286,55 @@ def moe_forward_fp8(x_bf16_rows, wg_bf16, w1q, w1s, w2q, w2s, K, wmap=None):
     y = np.empty((n, D), np.float32)
     wm = None if wmap is None else _c(wmap, np.int32)
     lib().orc_moe_forward_fp8(x, n, wg, w1q, w1s, w2q, w2s, _opt(wm), E, K, D, I, idx, wts, y)
+    return idx, wts, y
+
+
+# ---------------------------------------------------------------- MX (OCP microscaling)
+def e8m0_to_f32(c):
+    return float(lib().orc_e8m0_to_f32(int(c)))
+
+
+def e2m1_to_f32(c):
+    return float(lib().orc_e2m1_to_f32(int(c)))
+
+
+def f32_to_e2m1_scalar(v):
+    return int(lib().orc_f32_to_e2m1(float(v)))
+
+
+def mx_quant_rows(x, elem_bits):
+    """Rows -> (codes, E8M0 scales [rows, cols/32]); fp4 codes packed two per
+    byte (even element in the low nibble) [rows, cols/2], fp8 [rows, cols]."""
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    q = np.zeros((rows, cols // 2 if elem_bits == 4 else cols), np.uint8)
+    s = np.empty((rows, cols // 32), np.uint8)
+    lib().orc_mx_quant_rows(x, rows, cols, elem_bits, q, s)
+    return q, s
+
+
+def mx_dequant_rows(q, s, elem_bits):
+    q, s = _c(q, np.uint8), _c(s, np.uint8)
+    rows = s.shape[0]
+    cols = s.shape[1] * 32
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_mx_dequant_rows(q, s, rows, cols, elem_bits, out)
+    return out
+
+
+def moe_forward_mxfp4(x_bf16_rows, wg_bf16, w1q, w1s, w2q, w2s, K, wmap=None):
+    """MXFP4 expert weights (row-major E2M1 + E8M0 per 32), MXFP8 activations."""
+    x = _c(x_bf16_rows, np.uint16)
+    wg = _c(wg_bf16, np.uint16)
+    w1q, w1s, w2q, w2s = (_c(a, np.uint8) for a in (w1q, w1s, w2q, w2s))
+    n, D = x.shape
+    E = wg.shape[0]
+    I = w2q.shape[2] * 2
+    idx = np.empty((n, K), np.int32)
+    wts = np.empty((n, K), np.float32)
+    y = np.empty((n, D), np.float32)
+    wm = None if wmap is None else _c(wmap, np.int32)
+    lib().orc_moe_forward_mxfp4(x, n, wg, w1q, w1s, w2q, w2s, _opt(wm), E, K, D, I, idx, wts, y)
     return idx, wts, y
 
 

@@ -311,6 +311,93 @@ EXPORT void orc_moe_permute(const int* idx, int T, int K, int E,
  * mirror a storage precision of the intermediate activation:
  *   act_mode 0: fp32 (reference), 1: bf16 RNE, 2: e4m3 1x128 blocks.
  * w1/w2 are fp32 (already dequantised where applicable). */
+/* ------------------------------------------------------------------ */
+/* OCP Microscaling (MX) formats, OCP MX specification v1.0: a block of  */
+/* 32 elements shares one E8M0 scale X = 2^(E-127) (E = 255 is NaN);     */
+/* elements are FP4 E2M1 (0, 0.5, 1, 1.5, 2, 3, 4, 6 and negatives) or  */
+/* FP8 E4M3.  Conversion from fp32 (spec section 6.3): shared exponent =  */
+/* floor(log2(max |v|)) - emax_elem (E2M1: 2, E4M3: 8), clamped to the    */
+/* E8M0 range; each element = RNE(v / X), saturated to the element's     */
+/* largest normal.  No counterpart in the reference (fp32 only); the      */
+/* format of this build's MXFP4 expert weights and MXFP8 activations.     */
+/* An all-zero block gets E = 0.                                          */
+/* ------------------------------------------------------------------ */
+EXPORT float orc_e8m0_to_f32(uint8_t c) { return c == 255 ? NAN : ldexpf(1.0f, (int)c - 127); }
+
+/* E2M1: sign, 2 exponent bits (bias 1), 1 mantissa bit; exponent 0 is
+ * subnormal (m * 0.5). */
+EXPORT float orc_e2m1_to_f32(uint8_t c) {
+    int e = (c >> 1) & 3, m = c & 1;
+    float v = e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, e - 1);
+    return (c & 8) ? -v : v;
+}
+
+/* Round to nearest even E2M1, saturating at 6 (NaN also gives the largest
+ * magnitude: E2M1 has no NaN).  Within a binade the representable values
+ * are the multiples of a step (0.5 below 2, 1 in [2,4), 2 in [4,6]) whose
+ * parity is the mantissa bit, so RNE is rint on a / step. */
+EXPORT uint8_t orc_f32_to_e2m1(float f) {
+    uint8_t sign = signbit(f) ? 8 : 0;
+    float a = fabsf(f);
+    if (isnan(f) || a >= 6.0f) return sign | 7;
+    float step = a < 2.0f ? 0.5f : (a < 4.0f ? 1.0f : 2.0f);
+    float r = rintf(a / step) * step;
+    uint8_t code = r < 2.0f ? (uint8_t)(r * 2.0f) : (r < 4.0f ? (uint8_t)(4 + (int)(r - 2.0f))
+                                                             : (r < 6.0f ? 6 : 7));
+    return sign | code;
+}
+
+/* One 32-element block: returns the E8M0 code, writes the element codes
+ * (elem_bits 4: E2M1, one code per byte here; 8: E4M3). */
+static uint8_t mx_block(const float* v, int elem_bits, uint8_t* codes) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    int e8 = 0;
+    if (amax > 0.0f) {
+        int e;
+        frexpf(amax, &e);                      /* floor(log2 amax) = e - 1 */
+        e8 = e - 1 - (elem_bits == 4 ? 2 : 8) + 127;
+        if (e8 < 0) e8 = 0;
+        if (e8 > 254) e8 = 254;
+    }
+    float inv = ldexpf(1.0f, 127 - e8);        /* 1 / X, a power of two: exact */
+    for (int i = 0; i < 32; i++)
+        codes[i] = elem_bits == 4 ? orc_f32_to_e2m1(v[i] * inv) : orc_f32_to_e4m3(v[i] * inv);
+    return (uint8_t)e8;
+}
+
+/* Rows of cols values (cols % 32 == 0) -> MX: fp4 codes packed two per byte
+ * (element 2j in the low nibble) [rows, cols/2], or fp8 codes [rows, cols];
+ * scales E8M0 [rows, cols/32]. */
+EXPORT void orc_mx_quant_rows(const float* x, long rows, int cols, int elem_bits, uint8_t* q,
+                              uint8_t* s) {
+    uint8_t c[32];
+    for (long r = 0; r < rows; r++)
+        for (int b = 0; b < cols / 32; b++) {
+            s[r * (cols / 32) + b] = mx_block(x + r * cols + 32 * b, elem_bits, c);
+            for (int j = 0; j < 32; j++) {
+                long i = r * cols + 32 * b + j;
+                if (elem_bits == 4) {
+                    if (j & 1) q[i / 2] |= (uint8_t)(c[j] << 4);
+                    else q[i / 2] = c[j];
+                } else {
+                    q[i] = c[j];
+                }
+            }
+        }
+}
+
+EXPORT void orc_mx_dequant_rows(const uint8_t* q, const uint8_t* s, long rows, int cols,
+                                int elem_bits, float* out) {
+    for (long r = 0; r < rows; r++)
+        for (int j = 0; j < cols; j++) {
+            long i = r * cols + j;
+            float e = elem_bits == 4 ? orc_e2m1_to_f32((q[i / 2] >> (4 * (i & 1))) & 15)
+                                     : orc_e4m3_to_f32(q[i]);
+            out[i] = e * orc_e8m0_to_f32(s[r * (cols / 32) + j / 32]);
+        }
+}
+
 static void expert_ffn_rows(const float* xrows, int cnt, const float* w1_e, const float* w2_e,
                             int D, int I, int act_mode, float* g2 /* [cnt, D] */) {
     float* g1 = (float*)malloc(sizeof(float) * 2 * (size_t)I);
@@ -333,6 +420,13 @@ static void expert_ffn_rows(const float* xrows, int cnt, const float* w1_e, cons
         } else if (act_mode == 2) {
             orc_quant_rows_1x128(act, 1, I, q, sc);
             for (int j = 0; j < I; j++) act[j] = orc_e4m3_to_f32(q[j]) * sc[j / 128];
+        } else if (act_mode == 3) {
+            /* MXFP8: E4M3 elements, one E8M0 scale per 32 (the MXFP4 layer) */
+            for (int b = 0; b < I / 32; b++) {
+                const uint8_t e8 = mx_block(act + 32 * b, 8, q + 32 * b);
+                for (int j = 0; j < 32; j++)
+                    act[32 * b + j] = orc_e4m3_to_f32(q[32 * b + j]) * orc_e8m0_to_f32(e8);
+            }
         }
         /* GEMM2 tests/test_moe.cu:112-121 */
         #pragma omp parallel for schedule(static)
@@ -473,6 +567,54 @@ EXPORT void orc_moe_forward_fp8(const uint16_t* x, int n, const uint16_t* Wg,
         for (int m = 0; m < cnt; m++)
             memcpy(xr + (size_t)m * D, xf + (size_t)tmap[m] * D, sizeof(float) * (size_t)D);
         expert_ffn_rows(xr, cnt, w1f, w2f, D, I, 2, g2);
+        for (int m = 0; m < cnt; m++) {
+            int t = tmap[m];
+            float w = 0.0f;
+            for (int k = 0; k < K; k++)
+                if (idx[t * K + k] == e) { w = wts[t * K + k]; break; }
+            for (int d = 0; d < D; d++) y[(size_t)t * D + d] += w * g2[(size_t)m * D + d];
+        }
+    }
+    free(xf); free(wgf); free(xq); free(xs); free(tmap); free(xr); free(g2); free(w1f); free(w2f);
+}
+
+/* MXFP4 layer (this build's extension of the fp8 layer): expert weights
+ * E2M1 with E8M0 scales per 32 along K (W1 q [E',2I,D/2], s [E',2I,D/32];
+ * W2 q [E',D,I/2], s [E',D,I/32], row-major, element 2j in the low nibble),
+ * activations MXFP8 (x and the SwiGLU output quantised per 32 columns).
+ * Routing as orc_moe_forward_fp8 (bf16 x and gate); wmap as there. */
+EXPORT void orc_moe_forward_mxfp4(const uint16_t* x, int n, const uint16_t* Wg,
+                                  const uint8_t* w1q, const uint8_t* w1s,
+                                  const uint8_t* w2q, const uint8_t* w2s, const int* wmap,
+                                  int E, int K, int D, int I,
+                                  int* idx, float* wts, float* y) {
+    float* xf = (float*)malloc(sizeof(float) * (size_t)n * D);
+    float* wgf = (float*)malloc(sizeof(float) * (size_t)E * D);
+    orc_bf16_to_f32_array(x, xf, (long)n * D);
+    orc_bf16_to_f32_array(Wg, wgf, (long)E * D);
+    orc_moe_route(xf, wgf, NULL, n, E, K, D, idx, wts, NULL, NULL);
+    uint8_t* xq = (uint8_t*)malloc((size_t)n * D);
+    uint8_t* xs = (uint8_t*)malloc((size_t)n * (D / 32));
+    orc_mx_quant_rows(xf, n, D, 8, xq, xs);
+    orc_mx_dequant_rows(xq, xs, n, D, 8, xf);
+    memset(y, 0, sizeof(float) * (size_t)n * D);
+    int* tmap = (int*)malloc(sizeof(int) * (size_t)n);
+    float* xr = (float*)malloc(sizeof(float) * (size_t)n * D);
+    float* g2 = (float*)malloc(sizeof(float) * (size_t)n * D);
+    float* w1f = (float*)malloc(sizeof(float) * (size_t)2 * I * D);
+    float* w2f = (float*)malloc(sizeof(float) * (size_t)D * I);
+    for (int e = 0; e < E; e++) {
+        int cnt = 0;
+        for (int t = 0; t < n; t++)
+            for (int k = 0; k < K; k++)
+                if (idx[t * K + k] == e) { tmap[cnt++] = t; break; }
+        if (cnt == 0) continue;
+        size_t ws = wmap ? (size_t)wmap[e] : (size_t)e;
+        orc_mx_dequant_rows(w1q + ws * 2 * I * (D / 2), w1s + ws * 2 * I * (D / 32), 2 * I, D, 4, w1f);
+        orc_mx_dequant_rows(w2q + ws * D * (I / 2), w2s + ws * D * (I / 32), D, I, 4, w2f);
+        for (int m = 0; m < cnt; m++)
+            memcpy(xr + (size_t)m * D, xf + (size_t)tmap[m] * D, sizeof(float) * (size_t)D);
+        expert_ffn_rows(xr, cnt, w1f, w2f, D, I, 3, g2);
         for (int m = 0; m < cnt; m++) {
             int t = tmap[m];
             float w = 0.0f;

@@ -1,7 +1,8 @@
 """Static check of the grouped GEMM's asm weight loads.
 
 The weight loads of grouped_gemm_kernel are inline-asm
-`buffer_load_dwordx4 v[a:b], ...` (no `lds` modifier): the compiler does not
+`buffer_load_dwordx4 v[a:b], ...` and (MX scales) `buffer_load_ubyte v, ...`
+(no `lds` modifier): the compiler does not
 know they are still in flight, so nothing may read or overwrite their
 destination registers until an explicit `s_waitcnt vmcnt(...)`.  This walks
 every control-flow path from each such load (following branches) to the
@@ -33,7 +34,7 @@ def violations(asm_text):
         m = re.match(r"^(_Z\w+):$", ln)
         if m:
             kern = m.group(1)
-        m = re.match(r"buffer_load_dwordx4 (v\[\d+:\d+\]), ", ln)
+        m = re.match(r"buffer_load_(?:dwordx4|ubyte) (v\[\d+:\d+\]|v\d+), ", ln)
         if not m or ln.endswith(" lds"):
             continue
         dst = _regs(m.group(1))
@@ -54,7 +55,7 @@ def violations(asm_text):
                 if t.startswith("s_cbranch"):
                     stack.append(labels[t.split()[1]])
                 if t and not t.endswith(":") and not t.startswith(".") \
-                        and not t.startswith("buffer_load_dwordx4"):
+                        and not t.startswith("buffer_load_dwordx4") and not t.startswith("buffer_load_ubyte"):
                     ops = re.split(r"[ ,]+", t)[1:]
                     if set().union(set(), *[_regs(o) for o in ops]) & dst:
                         bad.append((kern, j + 1, t))
@@ -83,7 +84,7 @@ def sgpr_hazards(asm_text, states=5):
         m = re.match(r"^(_Z\w+):$", ln)
         if m:
             kern = m.group(1)
-        m = re.match(r"buffer_load_dwordx4 v\[\d+:\d+\], v\d+, (s\[\d+:\d+\]), (s\d+) offen", ln)
+        m = re.match(r"buffer_load_(?:dwordx4|ubyte) (?:v\[\d+:\d+\]|v\d+), v\d+, (s\[\d+:\d+\]), (s\d+) offen", ln)
         if not m:
             continue
         want = _sregs(m.group(1)) | _sregs(m.group(2))

@@ -46,7 +46,7 @@ def test_checker_follows_branches_to_a_use():
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc missing")
 def test_grouped_gemm_weight_loads_are_never_touched_in_flight(tmp_path):
-    assert len(SRCS) >= 5, SRCS
+    assert len(SRCS) >= 7, SRCS
     procs = []
     for src in SRCS:
         out = tmp_path / (os.path.basename(src)[:-4] + ".s")
@@ -60,6 +60,8 @@ def test_grouped_gemm_weight_loads_are_never_touched_in_flight(tmp_path):
         assert p.returncode == 0, (src, err[-2000:])
         asm = out.read_text()
         assert asm.count("buffer_load_dwordx4 v[") > 0, src
+        if "_mx_" in src:
+            assert asm.count("buffer_load_ubyte v") > 0, src
         bad = violations(asm)
         assert bad == [], (src, bad[:5])
         bad = sgpr_hazards(asm)
