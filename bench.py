@@ -169,6 +169,40 @@ def indexer_bench(amdmoe, synth, iters=20):
             "shape": f"Q={Q} Hi={Hi} ctx={ctx} top-{topk}"}
 
 
+def mxfp4_bench(amdmoe, synth, iters=20, tokens=(1, 64, 4096)):
+    """The MXFP4 expert layer (OCP MX: E2M1 weights, E4M3 activations, E8M0
+    scales per 32; no counterpart in the reference) at the DSV3 shape, per
+    token count: ms per layer, tokens/s, and the HBM floor of the bytes that
+    must cross (active experts' fp4 weights + scales, x, gate, y)."""
+    import torch
+    E, K, D, I = 256, 8, 7168, 2048
+    w1p, w1s, w2p, w2s = synth.mxfp4_weights(E, D, I, seed=1234)
+    xa, wg = synth.dsv3_inputs(max(tokens), E, D, seed=99)
+    rows = {}
+    for T in tokens:
+        x = xa[:T].contiguous()
+        cfg = amdmoe.moe_config(T, E, K, D, I)
+        ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_MXFP4)
+        y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+        idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+        wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+        amdmoe.moe_gate_bf16(x, wg, idx, wts, cfg)
+        torch.cuda.synchronize()
+        act = int(torch.unique(idx).numel())
+        ms = _time_calls(lambda: amdmoe.moe_forward_mxfp4(x, wg, w1p, w1s, w2p, w2s, y, cfg, ws=ws), iters)
+        nbytes = act * 3 * I * D * (0.5 + 1 / 32) + E * D * 2 + 2 * T * D * 2
+        flops = 6 * T * K * D * I
+        rows[f"T{T}"] = {"ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                         "experts_active": act, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                         "hbm_floor_ms": round(nbytes / HBM_PEAK * 1e3, 4),
+                         "floor_frac": round(nbytes / HBM_PEAK / (ms * 1e-3), 4)}
+        log(f"[bench] mxfp4 T={T}: {rows[f'T{T}']}")
+        del x, y, ws
+    del w1p, w1s, w2p, w2s, xa, wg
+    torch.cuda.empty_cache()
+    return rows
+
+
 def _time_calls(fn, iters, warmup=3):
     """Mean ms of fn() over iters calls, hip events on torch's current stream
     (the stream every amdmoe wrapper launches on by default)."""
@@ -276,6 +310,11 @@ def sweep(amdmoe, synth, iters):
         del x, y, ws
     del w1q, w1s, w2q, w2s, w1p, w2p, xa, wg
     torch.cuda.empty_cache()
+    for name, r in mxfp4_bench(amdmoe, synth, iters, tokens=(1, 64, 512, 4096, 8192)).items():
+        T = int(name[1:])
+        row(f"dsv3_mxfp4_{name}", "mxfp4", T, 256, 8, 7168, 2048, r["ms"],
+            r["experts_active"] * 3 * 2048 * 7168 * (0.5 + 1 / 32) + 256 * 7168 * 2, 2 * T * 7168 * 2,
+            FP8_PEAK, r["experts_active"])
     return rows
 
 
@@ -457,6 +496,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--cpu-sample", type=int, default=1024, help="tokens for the CPU baseline (0: skip)")
     ap.add_argument("--skip-dsa", action="store_true")
+    ap.add_argument("--skip-mx", action="store_true", help="skip the MXFP4 layer rows")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "moe_dsv3_fp8_T4096_traffic.json"),
                     help="measured HBM bytes per launch (FETCH_SIZE/WRITE_SIZE counter runs, "
                          "calibrated on a copy kernel; see the .md beside it)")
@@ -593,6 +633,9 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / (HBM_PEAK / 1e9), 4),
                      "traffic": round(traffic) if traffic else None, "algorithmic_bytes": up_bytes},
     }
+    if not args.skip_mx:
+        log("[bench] MXFP4 layer")
+        result["mxfp4_layer"] = mxfp4_bench(amdmoe, synth)
     if not args.skip_dsa:
         log("[bench] DSA decode")
         result["dsa_decode"] = dsa_bench(amdmoe, synth)

@@ -171,8 +171,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     constexpr bool kScaledA = DT == DT_FP8 || DT == DT_MX;  // activations carry row scales
     static_assert(DT != DT_MX || PK, "MX weights exist in fragment order only");
     using Frag = std::conditional_t<DT == DT_MX, BFragMx, BFrag>;
-    constexpr int kASlots = 4 + (kScaledA ? 1 : 0);
-    constexpr int kSlots = kASlots + 4;
+    // per K-step and wave: ceil(R/4) activation slabs of 8 rows (the 2R slabs
+    // of R live token tiles dealt round-robin over the 8 waves: slab s of
+    // wave w holds rows 64s + 8w .. +7), one scale slot (fp8 / MX), 4
+    // weight slots -- the same count for every wave, so no wave branches
+    // around its loads
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
 
@@ -227,13 +230,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     long arow[5];
 #pragma unroll
     for (int j = 0; j < 5; j++) {
-        const int r = j < 4 ? 32 * wave + 8 * j + lrow : 32 * wave + (lane & 31);
+        const int r = j < 4 ? 64 * j + 8 * wave + lrow : 32 * wave + (lane & 31);
         arow[j] = MODE == MODE_UP ? (long)g.a_map[row0 + min(r, rows - 1)] : (long)(row0 + r);
     }
-    uint32_t voff_a[4];
+    uint32_t voff_a[4];  // slab j of this wave: rows 64j + 8w .. +7
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int r = 32 * wave + 8 * j + lrow;
+        const int r = 64 * j + 8 * wave + lrow;
         voff_a[j] = r < rows ? (uint32_t)(arow[j] * g.a_row_bytes + 16 * lchunk) : kOob;
     }
     // activation scales of a K-step: fp8 one fp32 per row, MX the row's four
@@ -292,45 +295,52 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         return k >= nk ? k - nk : k;
     };
 
-    // Loads for a K-step past the end (kt >= nk) are still issued, with an
-    // out-of-range offset (they read zeros and touch no memory), so every
-    // step waits for the same vmcnt and no path through the loop skips a
-    // wait.  issue_slot(s, ...) issues one of the kSlots instructions of
-    // K-step kt into ring stage st / register set f.
-    // Activation slots load K-step kt_a into ring stage kt_a % kNS, weight
-    // slots load K-step kt_b into the register set f.
-    auto issue_slot = [&](int sl, bool a_live, int kt_a, int kt_b, Frag& f) __attribute__((always_inline)) {
-        if (sl < kASlots) {
-            if (!a_live) return;
-            const bool live = kt_a < nk;
-            const int kb = kblk(kt_a);
-            uint8_t* stage = smem + (kt_a % kNS) * kStageBytes;
-            if (sl < 4)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    ra, (lds_ptr_t)(stage + (32 * wave + 8 * sl) * 128), 16,
-                    live ? voff_a[sl] : kOob, kb * 128, 0, 0);
-            else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rs, (lds_ptr_t)(stage + kATile + wave * 256), 4,
-                    live ? voff_s : kOob, kb * 4, 0, 0);
+    // Loads for a K-step past the end (kt >= nk) are still issued, through
+    // a descriptor of zero bytes (they read zeros and touch no memory), so
+    // every step waits for the same vmcnt and no path through the loop skips
+    // a wait.  The scalar part of a step's addressing (rotated K block,
+    // soffsets, LDS stage, live or null descriptors) is formed once per step
+    // (STEP_ADDR); issue_slot(sl, ...) then issues slot sl of kSl: the
+    // activation slabs of K-step kt_a into ring stage kt_a % kNS, the scale
+    // slot, then the weight slots of K-step kt_b into register set f.
+    const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(g.a, 0), rs0 = make_rsrc(g.a, 0);
+    i32x4 rb0 = rb, rbs0 = rbs;
+    rb0[2] = 0;
+    rbs0[2] = 0;
+    // (the step's scalars: descriptors ra_/rs_/rb_/rbs_, soffsets so_*, LDS
+    // stage st_ -- declared by STEP_ADDR(kt_a, kt_b) where a slot is issued)
+#define STEP_ADDR(KT_A, KT_B)                                                              \
+    const bool live_a_ = (KT_A) < nk, live_b_ = (KT_B) < nk;                               \
+    const int ka_ = kblk(KT_A), kb_ = kblk(KT_B);                                          \
+    const __amdgpu_buffer_rsrc_t ra_ = live_a_ ? ra : ra0, rs_ = live_a_ ? rs : rs0;       \
+    const i32x4 rb_ = live_b_ ? rb : rb0, rbs_ = live_b_ ? rbs : rbs0;                     \
+    const int so_a = ka_ * 128, so_s = ka_ * 4, so_bs = kb_ * 64;                          \
+    const int so_b = DT == DT_MX ? kb_ * 1024 : (PK ? kb_ * 2048 : kb_ * 128);             \
+    uint8_t* const st_ = smem + ((KT_A) % kNS) * kStageBytes
+    auto issue_slot = [&](auto rc, int sl, __amdgpu_buffer_rsrc_t ra_, __amdgpu_buffer_rsrc_t rs_,
+                          i32x4 rb_, i32x4 rbs_, int so_a, int so_s, int so_b, int so_bs,
+                          uint8_t* st_, Frag& f) __attribute__((always_inline)) {
+        constexpr int NS = (decltype(rc)::value + 3) / 4;
+        constexpr int kAS = NS + (kScaledA ? 1 : 0);
+        if (sl < NS) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra_, (lds_ptr_t)(st_ + (64 * sl + 8 * wave) * 128), 16, voff_a[sl], so_a, 0, 0);
+        } else if (sl < kAS) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs_, (lds_ptr_t)(st_ + kATile + wave * 256), 4, voff_s, so_s, 0, 0);
         } else {
-            const bool live = kt_b < nk;
-            const int kb = kblk(kt_b);
-            const int ct = (sl - kASlots) >> 1;
+            const int ct = (sl - kAS) >> 1;
             if constexpr (DT == DT_MX) {
                 // 1 KB of E2M1 (16 rows x 128 K) and the 64 scale bytes of the block
-                if ((sl - kASlots) & 1)
-                    f.s[ct] = buffer_load_u8_async(rbs, live ? voff_bs[ct] : kOob, kb * 64);
-                else
-                    f.w[ct] = buffer_load_b128_async<0>(rb, live ? voff_b[ct] : kOob, kb * 1024);
+                if ((sl - kAS) & 1) f.s[ct] = buffer_load_u8_async(rbs_, voff_bs[ct], so_bs);
+                else f.w[ct] = buffer_load_b128_async<0>(rb_, voff_b[ct], so_b);
             } else {
-                const uint32_t vo = live ? voff_b[ct] : kOob;
-                const int sstep = PK ? kb * 2048 : kb * 128;
-                if ((sl - kASlots) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb, vo, sstep + (PK ? 1024 : 64));
-                else f.q[ct][0] = buffer_load_b128_async<0>(rb, vo, sstep);
+                if ((sl - kAS) & 1) f.q[ct][1] = buffer_load_b128_async<0>(rb_, voff_b[ct], so_b + (PK ? 1024 : 64));
+                else f.q[ct][0] = buffer_load_b128_async<0>(rb_, voff_b[ct], so_b);
             }
         }
     };
+#define SLOT_ARGS ra_, rs_, rb_, rbs_, so_a, so_s, so_b, so_bs, st_
 
     const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
 
@@ -468,26 +478,24 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // a wave's loads only as fast as it drains them, so issuing all of a
     // step's loads at once parks every wave at the issue for most of the
     // step.  Slot s goes out right after the MFMAs of token tile
-    // (s * tiles) / kSlots, so the activation slots go first.
-    auto step = [&](auto stc, auto rc, auto rbc, bool a_live, int kt, Frag& cur, Frag& refill)
+    // (s * tiles) / kSl, so the activation slots go first.
+    auto step = [&](auto stc, auto rc, auto rbc, int kt, Frag& cur, Frag& refill)
                     __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;  // token tiles per step
         constexpr int RB = decltype(rbc)::value;
+        constexpr int kSl = (R + 3) / 4 + (kScaledA ? 1 : 0) + 4;
         // Issue order per step: activation slots of step kt+2, then the 4
         // weight loads of step kt+RB-1.  Everything of step kt has landed
         // once at most kWait vector-memory instructions are outstanding:
-        //   RB == 5: the weights of steps kt+1..kt+3 (12) -- for a wave
-        //            with activation slots this also covers the activations
-        //            of step kt, which precede 4 + kASlots + 4 >= 12 later
-        //            instructions;
+        //   RB == 5: the weights of steps kt+1..kt+3 (12), which also
+        //            covers the activations of step kt (they precede the
+        //            weights of steps kt+1..kt+3);
         //   RB == 3: the weights of step kt+1 (4), which follow the
         //            activations of step kt+1 (those are thus waited for
         //            one step early).
-        //   RB == 4: the weights of steps kt+1, kt+2 (8) -- for a wave with
-        //            activation slots, whose step-kt activations precede
-        //            4 + kASlots + 4 later instructions, this also waits for
-        //            the first activation slot of step kt+1 (one count for
-        //            all waves: no path mixes the two).
+        //   RB == 4: the last 8 issued (the weights of step kt+2 and the
+        //            newest activation slots of step kt+1): the weights of
+        //            step kt and the activations of step kt precede them.
         //   RB == 2: the weights of step kt were the last loads issued, so
         //            nothing may be outstanding (the activations of step
         //            kt+1, issued before them, are waited for one step early).
@@ -497,9 +505,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
         bare_barrier();
+        STEP_ADDR(kt + 2, kt + RB - 1);
         auto tile_issued = [&](int rt) __attribute__((always_inline)) {
-            for (int sl = 0; sl < kSlots; sl++)
-                if ((sl * R) / kSlots == rt) issue_slot(sl, a_live, kt + 2, kt + RB - 1, refill);
+            for (int sl = 0; sl < kSl; sl++)
+                if ((sl * R) / kSl == rt) issue_slot(rc, sl, SLOT_ARGS, refill);
         };
         compute(rc, cur, kt, tile_issued);
     };
@@ -511,7 +520,6 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         constexpr int R = decltype(rc)::value;
         constexpr int RB = R <= 12 ? kRbSmall : kRbLarge;
         const std::integral_constant<int, RB> rbc;
-        const bool a_live = 32 * wave < 16 * R;  // uniform
         // only the live token tiles' accumulators exist during the loop
 #pragma unroll
         for (int i = 0; i < R; i++)
@@ -522,13 +530,15 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // 0..RB-2)
         static_for<(RB - 1 > 2 ? RB - 1 : 2)>([&](auto ic) __attribute__((always_inline)) {
             constexpr int i = decltype(ic)::value;
-            for (int sl = 0; sl < kSlots; sl++)
-                if (sl < kASlots ? i < 2 : i < RB - 1) issue_slot(sl, a_live, i, i, bs[i < RB ? i : 0]);
+            constexpr int kAS = (R + 3) / 4 + (kScaledA ? 1 : 0);
+            STEP_ADDR(i, i);
+            for (int sl = 0; sl < kAS + 4; sl++)
+                if (sl < kAS ? i < 2 : i < RB - 1) issue_slot(rc, sl, SLOT_ARGS, bs[i < RB ? i : 0]);
         });
         for (int kt = 0; kt < nk; kt += RB) {
             static_for<RB>([&](auto stc) __attribute__((always_inline)) {
                 constexpr int ST = decltype(stc)::value;
-                if (ST == 0 || kt + ST < nk) step(stc, rc, rbc, a_live, kt + ST, bs[ST], bs[(ST + RB - 1) % RB]);
+                if (ST == 0 || kt + ST < nk) step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB]);
             });
         }
         // drain the trailing (out-of-range) prefetches before the ring and
@@ -539,6 +549,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         for (int i = R; i < 16; i++)
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     };
+#undef STEP_ADDR
+#undef SLOT_ARGS
     // The loop is instantiated per live token-tile count: fp8 and MX (the
     // layer's headline paths, where an expert's 128 +- 11 rows would
     // otherwise be rounded up to 192) in steps of one 16-row tile, the fp32 /

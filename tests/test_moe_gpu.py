@@ -333,7 +333,9 @@ def _bf16_case(amd, orc, T, E, K, D, I, bias, sample=None, seed=7):
 def bf16_steps(got, ref):
     """Largest |got - ref| in units of one bf16 step (2^-7 of the binade) at
     ref: the output is bf16, so its own rounding is half a step."""
-    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -100))) - 7)
+    # (values below 2^-7 count with the step at 2^-7: a 1e-2 absolute bar
+    # governs them)
+    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -7))) - 7)
     return float((np.abs(got - ref) / step).max())
 
 
