@@ -186,8 +186,17 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     if (slot >= per) return;
     const int w = (blockIdx.x & 7) * per + slot;
     if (w >= W) return;
-    const int mt = w / g.n_tiles_n, nt = w - mt * g.n_tiles_n;
-    const int4 tile = g.tiles[mt];
+    // An expert with m M-tiles owns items [f*ntn, (f+m)*ntn) (f its first
+    // tile), ordered N-tile major: item f*ntn + m*nt + j is (tile f+j, nt),
+    // so the m tiles that read the same weight tile are dispatched back to
+    // back on one XCD and share its weight stream through L2.
+    const int ntn = g.n_tiles_n;
+    const int mt0 = w / ntn;  // a tile of the owning expert
+    const int4 tile0 = g.tiles[mt0];
+    const int m_tiles = tile0.w & 0xffff, first_tile = mt0 - (tile0.w >> 16);
+    const int l_item = w - first_tile * ntn;
+    const int nt = l_item / m_tiles, mt = first_tile + (l_item - nt * m_tiles);
+    const int4 tile = m_tiles == 1 ? tile0 : g.tiles[mt];
     const int e = tile.x, row0 = tile.y, rows = tile.z;
     const int nk = (int)((long)g.K * ES / 128);
     const int kb_per_row = g.K / 128;  // fp8 scale blocks along K

@@ -26,14 +26,16 @@ constexpr int kPermThreads = 1024;
 // M-tile j of an expert with `cnt` rows starting at row_off: the expert's
 // ceil(cnt / BM) tiles split its 16-row token tiles as evenly as possible
 // (270 rows -> 144 + 126, not 256 + 14), so the tiles of one expert run
-// at the same pace and stream its weights side by side.
+// at the same pace and stream its weights side by side.  .w = (j << 16) |
+// the expert's tile count: the GEMMs order an expert's work items N-tile
+// major over its M-tiles with it.
 __device__ __forceinline__ int4 mtile(int e, int row_off, int cnt, int BM, int j) {
     const int nt = (cnt + BM - 1) / BM;
     const int q = (cnt + 15) / 16;  // token tiles
     const int base = q / nt, extra = q % nt;
     const int first = 16 * (j * base + min(j, extra));
     const int rows = min(16 * (base + (j < extra ? 1 : 0)), cnt - first);
-    return make_int4(e, row_off + first, rows, 0);
+    return make_int4(e, row_off + first, rows, (j << 16) | nt);
 }
 
 // Slot i = t*K + k counts for expert e = idx[i] only if no earlier slot of
