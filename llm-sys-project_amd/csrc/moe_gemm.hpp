@@ -38,9 +38,10 @@
 // (~96 KB per CU) are in flight while one is consumed.  Waits are explicit vmcnt counts and the barrier is a bare
 // s_barrier, so nothing drains mid-loop.
 //
-// Work items are laid out M-tile-major (all N-tiles of an M-tile are
-// consecutive) and dealt to XCDs in contiguous chunks (workgroup b runs on
-// XCD b % 8), so an M-tile's activation rows stay in one XCD's L2.
+// Work items are laid out expert by expert, N-tile major over the expert's
+// M-tiles (the M-tiles that read one weight tile are consecutive), and dealt
+// to XCDs in contiguous chunks (workgroup b runs on XCD b % 8), so an
+// expert's activation rows and weight tiles stay in one XCD's L2.
 //
 // The kernel template lives in this header; each moe_gemm_<type>.hip file
 // instantiates some of its variants (the fp8 ones are large: one main loop
@@ -195,9 +196,12 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     const int4 tile0 = g.tiles[mt0];
     const int m_tiles = tile0.w & 0xffff, first_tile = mt0 - (tile0.w >> 16);
     const int l_item = w - first_tile * ntn;
-    const int nt = l_item / m_tiles, mt = first_tile + (l_item - nt * m_tiles);
+    const int nt = __builtin_amdgcn_readfirstlane(l_item / m_tiles);
+    const int mt = first_tile + (l_item - nt * m_tiles);
     const int4 tile = m_tiles == 1 ? tile0 : g.tiles[mt];
-    const int e = tile.x, row0 = tile.y, rows = tile.z;
+    // uniform values (SGPRs): the asm loads take their soffsets from them
+    const int e = __builtin_amdgcn_readfirstlane(tile.x), row0 = __builtin_amdgcn_readfirstlane(tile.y),
+              rows = __builtin_amdgcn_readfirstlane(tile.z);
     const int nk = (int)((long)g.K * ES / 128);
     const int kb_per_row = g.K / 128;  // fp8 scale blocks along K
 
@@ -612,8 +616,14 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const int rr = 128 * half + er;
             const int col = nt * 128 + 32 * pp;
             const bool ok = rr < rows && col < g.n_out;
+            // eight unconditional 16-byte reads (the staged row is in LDS
+            // whether or not it is stored), zeroed where not stored
             float v[32];
-            for (int j = 0; j < 32; j++) v[j] = ok ? Tb[er * kEpiPitch + 32 * pp + j] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const f32x4 t = *(const f32x4*)&Tb[er * kEpiPitch + 32 * pp + 4 * j];
+                for (int i = 0; i < 4; i++) v[4 * j + i] = ok ? t[i] : 0.0f;
+            }
             const size_t pos = (size_t)row0 + rr;
             if (DT == DT_FP8) {
                 float amax = 0.0f;
@@ -723,7 +733,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     }
                 }
                 lds_barrier();
-#pragma unroll
+    #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int c = tid + 512 * j;       // 16-byte chunk of the pass
                     const int rr = c >> 5, ch = c & 31;  // row in the pass, chunk in the row
