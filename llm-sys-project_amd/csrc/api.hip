@@ -46,6 +46,7 @@ struct MoeWs {
     float* sorted_w;
     uint8_t* xq;
     float* xs;
+    float* xs_sorted;  // xs gathered to sorted row order, K-step major (the UP GEMM's scales)
     uint8_t* act;
     float* act_s;
     uint8_t* ypair;
@@ -84,6 +85,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
         // per 32 -- the same bytes per row
         w.xq = take(T * D);
         w.xs = (float*)take(4 * T * (D / 128));
+        w.xs_sorted = (float*)take(4 * P * (D / 128));
         w.act = take(P * I);
         w.act_s = (float*)take(4 * P * (I / 128));
         w.ypair = take(2 * P * D);
@@ -206,13 +208,18 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
         TRY(mark(5, st));
         return mark(6, st);
     }
+    // fp8 / MX: the activation scales K-step major in sorted row order
+    if (x_scale)
+        TRY(launch_gather_row_scales((const uint32_t*)x_scale, w.sorted_token, P, T, D / 128,
+                                     (uint32_t*)w.xs_sorted, st));
     GemmArgs up{};
     up.a = a_x;
     up.a_bytes = (long)T * D * es;
     up.a_row_bytes = (long)D * es;
     up.a_map = w.sorted_token;
-    up.a_scale = x_scale;
-    up.a_scale_bytes = x_scale ? (long)T * (D / 128) * 4 : 0;
+    up.a_scale = x_scale ? w.xs_sorted : nullptr;
+    up.a_scale_bytes = x_scale ? P * (D / 128) * 4 : 0;
+    up.a_scale_rows = P;
     up.b = w1;
     up.b_expert_bytes = 2L * I * D * es / wdiv;
     up.b_row_bytes = (long)D * es / wdiv;
@@ -228,6 +235,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     up.n_tiles_n = (int)ceil_div(I, 128);
     up.out = w.act;
     up.out_scale = w.act_s;
+    up.out_scale_rows = P;
     TRY(launch_grouped_gemm(dt, MODE_UP, up, mtiles, st));
     TRY(mark(4, st));
     GemmArgs dn{};
@@ -236,6 +244,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.a_row_bytes = (long)I * es;
     dn.a_scale = w.act_s;
     dn.a_scale_bytes = w.act_s ? P * (I / 128) * 4 : 0;
+    dn.a_scale_rows = P;
     dn.b = w2;
     dn.b_expert_bytes = (long)D * I * es / wdiv;
     dn.b_row_bytes = (long)I * es / wdiv;

@@ -170,6 +170,13 @@ __device__ __forceinline__ void bare_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// This wave's LDS operations have completed (lgkmcnt(0) only).
+__device__ __forceinline__ void lds_wait() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14));
+    asm volatile("" ::: "memory");
+}
+
 // LDS writes issued before it are visible to every wave after it: waits for
 // this wave's LDS operations only (lgkmcnt(0); vector-memory and export
 // counters unconstrained, so direct-to-LDS loads keep flowing), then

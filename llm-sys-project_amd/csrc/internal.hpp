@@ -16,8 +16,9 @@ struct GemmArgs {
     long a_bytes;            // bytes of the whole A array (buffer range)
     long a_row_bytes;        // bytes per A row
     const int* a_map;        // UP: sorted_token (A row of sorted position); DOWN: unused
-    const float* a_scale;    // fp8: [A rows][K/128]
-    long a_scale_bytes;      // fp8: bytes of the whole a_scale array
+    const float* a_scale;    // fp8 / MX: [K/128][a_scale_rows] dwords, rows in sorted order
+    long a_scale_bytes;      // fp8 / MX: bytes of the whole a_scale array
+    long a_scale_rows;       // fp8 / MX: dwords per K-step of a_scale
     const uint8_t* b;        // expert weights base
     long b_expert_bytes;     // bytes per expert
     long b_row_bytes;        // bytes per weight row (K * element size)
@@ -30,14 +31,22 @@ struct GemmArgs {
     const int* num_tiles;    // device count of M-tiles
     int n_tiles_n;           // N-tiles per M-tile
     uint8_t* out;            // UP: act [P, I]; DOWN: ypair [T*K, D]
-    float* out_scale;        // UP fp8: act scales [P, I/128]
+    float* out_scale;        // UP fp8 / MX: act scales [I/128][out_scale_rows] dwords
+    long out_scale_rows;     // UP fp8 / MX: dwords per 128-column block of out_scale
     const int* sorted_slot;  // DOWN: flat slot t*K+k of each sorted row
     const float* sorted_w;   // DOWN: routing weight of each sorted row
     // MX only: E8M0 weight scales in fragment order [E][b_rows/16][K/128][64]
-    // (a_scale then holds the activations' E8M0 scales, [A rows][K/32] bytes)
+    // (a_scale then holds the activations' E8M0 scales, four bytes -- the
+    // 32-blocks of a 128-K step -- per dword)
     const uint8_t* b_mx_scale;
     long b_mx_scale_expert_bytes;
 };
+
+// moe_permute.hip: dst[kb * P + p] = src[sorted_token[p] * nkb + kb] (4-byte
+// elements, p < P): per-row block scales gathered into sorted row order,
+// K-step major (the grouped GEMM's a_scale layout)
+int launch_gather_row_scales(const uint32_t* src, const int* sorted_token, long P, int T, int nkb,
+                             uint32_t* dst, hipStream_t st);
 
 // moe_route.hip
 template <typename XT, typename GT>

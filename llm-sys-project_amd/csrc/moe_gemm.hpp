@@ -66,6 +66,11 @@ constexpr int kMaxKb = 128;                            // K <= 16384 on the fp8 
 // weight register sets of the main loop's ring (RB - 1 K-steps of weights in
 // flight) for up to 12 live token tiles and for more
 constexpr int kRbSmall = 4, kRbLarge = 3;
+// fp8 / MX M-tiles of up to this many 16-row token tiles stage their
+// activations through registers (global -> VGPR -> ds_write) instead of the
+// LDS DMA: measured cheaper per byte, and the registers are there while the
+// accumulators are few
+constexpr int kVgMaxR = 10;
 constexpr int kEpiPitch = 132;                         // floats per staged output row
 constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
 constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
@@ -104,6 +109,10 @@ __device__ __forceinline__ void pin(BFragMx& f) {
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void pin3(u32x4 (&a)[3]) {
+    asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]));
+}
 
 // 16-byte buffer load into registers, issued as inline asm so the compiler
 // does not insert its own vector-memory waits before the (much later) use;
@@ -240,10 +249,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     }
     // UP gathers the rows through a_map (index clamped to a live row; the
     // offset of a row past the tile is replaced by the out-of-range one)
-    long arow[5];
+    long arow[4];
 #pragma unroll
-    for (int j = 0; j < 5; j++) {
-        const int r = j < 4 ? 64 * j + 8 * wave + lrow : 32 * wave + (lane & 31);
+    for (int j = 0; j < 4; j++) {
+        const int r = 64 * j + 8 * wave + lrow;
         arow[j] = MODE == MODE_UP ? (long)g.a_map[row0 + min(r, rows - 1)] : (long)(row0 + r);
     }
     uint32_t voff_a[4];  // slab j of this wave: rows 64j + 8w .. +7
@@ -253,12 +262,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         voff_a[j] = r < rows ? (uint32_t)(arow[j] * g.a_row_bytes + 16 * lchunk) : kOob;
     }
     // activation scales of a K-step: fp8 one fp32 per row, MX the row's four
-    // E8M0 bytes -- both one dword per row and step, [rows][K/128] dwords
+    // E8M0 bytes -- both one dword per row and step, stored K-step major in
+    // sorted row order ([K/128][a_scale_rows] dwords), so the 32 rows of a
+    // wave's scale slot are one 128-byte line (row-major, every gathered
+    // row's scale was a line of its own: UP 8% slower)
     uint32_t voff_s = kOob;
     if (kScaledA) {
         const int r = 32 * wave + lane;
-        if (lane < 32 && r < rows) voff_s = (uint32_t)(arow[4] * kb_per_row * 4);
+        if (lane < 32 && r < rows) voff_s = (uint32_t)((row0 + r) * 4);
     }
+    const int scale_kstride = (int)(g.a_scale_rows * 4);  // bytes per K-step of a_scale
 
     // ---- weight rows of this wave: two MFMA column tiles of 16 ----
     //   UP:   ct 0 = gate rows n0 + 16w + c, ct 1 = up rows I + n0 + 16w + c
@@ -320,24 +333,33 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     i32x4 rb0 = rb, rbs0 = rbs;
     rb0[2] = 0;
     rbs0[2] = 0;
+    // the activation descriptor as words, for the register path's asm loads
+    const i32x4 rav = make_rsrc_words(g.a, g.a_bytes);
+    i32x4 rav0 = rav;
+    rav0[2] = 0;
     // (the step's scalars: descriptors ra_/rs_/rb_/rbs_, soffsets so_*, LDS
     // stage st_ -- declared by STEP_ADDR(kt_a, kt_b) where a slot is issued)
-#define STEP_ADDR(KT_A, KT_B)                                                              \
-    const bool live_a_ = (KT_A) < nk, live_b_ = (KT_B) < nk;                               \
-    const int ka_ = kblk(KT_A), kb_ = kblk(KT_B);                                          \
+#define STEP_ADDR(KT_A, KT_B, KT_V)                                                        \
+    const bool live_a_ = (KT_A) < nk, live_b_ = (KT_B) < nk, live_v_ = (KT_V) < nk;        \
+    const int ka_ = kblk(KT_A), kb_ = kblk(KT_B), kv_ = kblk(KT_V);                        \
     const __amdgpu_buffer_rsrc_t ra_ = live_a_ ? ra : ra0, rs_ = live_a_ ? rs : rs0;       \
     const i32x4 rb_ = live_b_ ? rb : rb0, rbs_ = live_b_ ? rbs : rbs0;                     \
-    const int so_a = ka_ * 128, so_s = ka_ * 4, so_bs = kb_ * 64;                          \
+    const i32x4 rv_ = live_v_ ? rav : rav0;                                                \
+    const int so_a = ka_ * 128, so_s = ka_ * scale_kstride, so_bs = kb_ * 64, so_v = kv_ * 128; \
     const int so_b = DT == DT_MX ? kb_ * 1024 : (PK ? kb_ * 2048 : kb_ * 128);             \
     uint8_t* const st_ = smem + ((KT_A) % kNS) * kStageBytes
     auto issue_slot = [&](auto rc, int sl, __amdgpu_buffer_rsrc_t ra_, __amdgpu_buffer_rsrc_t rs_,
-                          i32x4 rb_, i32x4 rbs_, int so_a, int so_s, int so_b, int so_bs,
-                          uint8_t* st_, Frag& f) __attribute__((always_inline)) {
-        constexpr int NS = (decltype(rc)::value + 3) / 4;
+                          i32x4 rb_, i32x4 rbs_, i32x4 rv_, int so_a, int so_s, int so_b, int so_bs,
+                          int so_v, uint8_t* st_, Frag& f, u32x4 (&av)[3]) __attribute__((always_inline)) {
+        constexpr int R = decltype(rc)::value;
+        constexpr int NS = (R + 3) / 4;
         constexpr int kAS = NS + (kScaledA ? 1 : 0);
         if (sl < NS) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra_, (lds_ptr_t)(st_ + (64 * sl + 8 * wave) * 128), 16, voff_a[sl], so_a, 0, 0);
+            if constexpr (kScaledA && R <= kVgMaxR)  // register path: K-step KT_V into av
+                av[sl < 3 ? sl : 0] = buffer_load_b128_async<0>(rv_, voff_a[sl], so_v);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra_, (lds_ptr_t)(st_ + (64 * sl + 8 * wave) * 128), 16, voff_a[sl], so_a, 0, 0);
         } else if (sl < kAS) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rs_, (lds_ptr_t)(st_ + kATile + wave * 256), 4, voff_s, so_s, 0, 0);
@@ -353,7 +375,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
         }
     };
-#define SLOT_ARGS ra_, rs_, rb_, rbs_, so_a, so_s, so_b, so_bs, st_
+#define SLOT_ARGS ra_, rs_, rb_, rbs_, rv_, so_a, so_s, so_b, so_bs, so_v, st_
 
     const int off_lo = 16 * (q ^ (r16 & 7)), off_hi = 16 * ((4 + q) ^ (r16 & 7));
 
@@ -492,11 +514,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // step's loads at once parks every wave at the issue for most of the
     // step.  Slot s goes out right after the MFMAs of token tile
     // (s * tiles) / kSl, so the activation slots go first.
-    auto step = [&](auto stc, auto rc, auto rbc, int kt, Frag& cur, Frag& refill)
-                    __attribute__((always_inline)) {
+    auto step = [&](auto stc, auto rc, auto rbc, int kt, Frag& cur, Frag& refill, u32x4 (&av_w)[3],
+                    u32x4 (&av_l)[3]) __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;  // token tiles per step
         constexpr int RB = decltype(rbc)::value;
-        constexpr int kSl = (R + 3) / 4 + (kScaledA ? 1 : 0) + 4;
+        constexpr int NS = (R + 3) / 4;
+        constexpr int kSl = NS + (kScaledA ? 1 : 0) + 4;
+        constexpr bool kVg = kScaledA && R <= kVgMaxR;
         // Issue order per step: activation slots of step kt+2, then the 4
         // weight loads of step kt+RB-1.  Everything of step kt has landed
         // once at most kWait vector-memory instructions are outstanding:
@@ -512,16 +536,32 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         //   RB == 2: the weights of step kt were the last loads issued, so
         //            nothing may be outstanding (the activations of step
         //            kt+1, issued before them, are waited for one step early).
+        //   register path (kVg, RB == 4): per step the activations of
+        //            step kt+3 go to registers (NS loads), the scale slot of
+        //            step kt+2, the weights of step kt+3.  At the top of step
+        //            kt the activations of step kt+1 (issued at step kt-2) are
+        //            written to LDS, so at most the NS + 5 loads of step kt-1
+        //            and the 4 weight loads of step kt-2 may be outstanding.
         static_assert(RB >= 2 && RB <= 5, "wait counts are derived for rings of 2 to 5 sets");
-        wait_vmcnt<RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0))>();
+        static_assert(!kVg || RB == 4, "the register path's wait count is derived for RB == 4");
+        wait_vmcnt<kVg ? NS + 9 : (RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0)))>();
         // the weights of this step have landed: pin every use of them below
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
+        if constexpr (kVg) {
+            // activations of step kt+1 -> LDS stage (kt+1) % 3, the slab
+            // layout the DMA would give (lane l's 16 bytes at 16 l); that
+            // stage was last read at step kt-2, which every wave has left
+            pin3(av_w);
+            uint8_t* stw = smem + ((kt + 1) % kNS) * kStageBytes + 8 * wave * 128 + 16 * lane;
+#pragma unroll
+            for (int sl = 0; sl < NS; sl++) *(u32x4*)(stw + 64 * sl * 128) = av_w[sl];
+        }
         bare_barrier();
-        STEP_ADDR(kt + 2, kt + RB - 1);
+        STEP_ADDR(kt + 2, kt + RB - 1, kt + 3);
         auto tile_issued = [&](int rt) __attribute__((always_inline)) {
             for (int sl = 0; sl < kSl; sl++)
-                if ((sl * R) / kSl == rt) issue_slot(rc, sl, SLOT_ARGS, refill);
+                if ((sl * R) / kSl == rt) issue_slot(rc, sl, SLOT_ARGS, refill, av_l);
         };
         compute(rc, cur, kt, tile_issued);
     };
@@ -538,26 +578,71 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         for (int i = 0; i < R; i++)
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
         Frag bs[RB];
-        // prologue, in the steady-state issue order: per step the
-        // activation slots (steps 0, 1) before the weight slots (steps
-        // 0..RB-2)
-        static_for<(RB - 1 > 2 ? RB - 1 : 2)>([&](auto ic) __attribute__((always_inline)) {
-            constexpr int i = decltype(ic)::value;
-            constexpr int kAS = (R + 3) / 4 + (kScaledA ? 1 : 0);
-            STEP_ADDR(i, i);
-            for (int sl = 0; sl < kAS + 4; sl++)
-                if (sl < kAS ? i < 2 : i < RB - 1) issue_slot(rc, sl, SLOT_ARGS, bs[i < RB ? i : 0]);
-        });
-        for (int kt = 0; kt < nk; kt += RB) {
-            static_for<RB>([&](auto stc) __attribute__((always_inline)) {
-                constexpr int ST = decltype(stc)::value;
-                if (ST == 0 || kt + ST < nk) step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB]);
+        constexpr int NS = (R + 3) / 4;
+        constexpr bool kVg = kScaledA && R <= kVgMaxR;
+        u32x4 av[2][3];  // register path: activations of odd / even K-steps
+        if constexpr (kVg) {
+            // prologue of the register path: groups (activations, scale,
+            // weights) of steps 0 and 1; the activations of step 0 -> LDS
+            // stage 0 once landed (the NS + 10 newer loads may be
+            // outstanding); then the activations and weights of step 2
+            // (set 0 is free again).  Step j then issues the activations
+            // and weights of step j+3 and the scale of step j+2.
+            static_for<2>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                STEP_ADDR(i, i, i);
+                for (int sl = 0; sl < NS + 5; sl++) issue_slot(rc, sl, SLOT_ARGS, bs[i], av[i]);
+            });
+            wait_vmcnt<NS + 10>();
+            pin3(av[0]);
+            {
+                uint8_t* stw = smem + 8 * wave * 128 + 16 * lane;
+#pragma unroll
+                for (int sl = 0; sl < NS; sl++) *(u32x4*)(stw + 64 * sl * 128) = av[0][sl];
+            }
+            {
+                STEP_ADDR(2, 2, 2);
+                for (int sl = 0; sl < NS + 5; sl++)
+                    if (sl != NS) issue_slot(rc, sl, SLOT_ARGS, bs[2], av[0]);
+            }
+            lds_wait();  // stage 0 written before step 0's barrier
+        } else {
+            // prologue, in the steady-state issue order: per step the
+            // activation slots (steps 0, 1) before the weight slots (steps
+            // 0..RB-2)
+            static_for<(RB - 1 > 2 ? RB - 1 : 2)>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int i = decltype(ic)::value;
+                constexpr int kAS = NS + (kScaledA ? 1 : 0);
+                STEP_ADDR(i, i, i);
+                for (int sl = 0; sl < kAS + 4; sl++)
+                    if (sl < kAS ? i < 2 : i < RB - 1) issue_slot(rc, sl, SLOT_ARGS, bs[i < RB ? i : 0], av[0]);
             });
         }
+        // whole groups of RB steps, then the < RB remaining ones (the loop's
+        // back edge is taken only after a full group, so no path re-enters
+        // it with a ring set still in flight that the next group reuses);
+        // kt is a multiple of RB at every group start (RB is even on the
+        // register path, so kt's parity is ST's)
+        int kt = 0;
+        for (; kt + RB <= nk; kt += RB) {
+            static_for<RB>([&](auto stc) __attribute__((always_inline)) {
+                constexpr int ST = decltype(stc)::value;
+                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[(ST + 1) & 1], av[(ST + 1) & 1]);
+            });
+        }
+        static_for<RB - 1>([&](auto stc) __attribute__((always_inline)) {
+            constexpr int ST = decltype(stc)::value;
+            if (kt + ST < nk)
+                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[(ST + 1) & 1], av[(ST + 1) & 1]);
+        });
         // drain the trailing (out-of-range) prefetches before the ring and
         // the weight registers are reused
         wait_vmcnt<0>();
         static_for<RB>([&](auto ic) __attribute__((always_inline)) { pin(bs[decltype(ic)::value]); });
+        if constexpr (kVg) {
+            pin3(av[0]);
+            pin3(av[1]);
+        }
 #pragma unroll
         for (int i = R; i < 16; i++)
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -646,7 +731,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     uint8_t* dst = g.out + pos * g.n_out + col;
                     *(u32x4*)dst = o0;
                     *(u32x4*)(dst + 16) = o1;
-                    if (pp == 0) g.out_scale[pos * (g.n_out / 128) + nt] = s;
+                    if (pp == 0) g.out_scale[(size_t)nt * g.out_scale_rows + pos] = s;
                 }
             } else if (DT == DT_MX) {
                 // MXFP8 (OCP MX): the thread's 32 columns are one block;
@@ -668,7 +753,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     uint8_t* dst = g.out + pos * g.n_out + col;
                     *(u32x4*)dst = o0;
                     *(u32x4*)(dst + 16) = o1;
-                    ((uint8_t*)g.out_scale)[pos * (g.n_out / 32) + col / 32] = (uint8_t)e8;
+                    ((uint8_t*)g.out_scale)[((size_t)(col / 128) * g.out_scale_rows + pos) * 4 + (col / 32) % 4] =
+                        (uint8_t)e8;
                 }
             } else if (DT == DT_BF16) {
                 if (ok) {

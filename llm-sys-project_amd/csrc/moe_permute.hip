@@ -555,4 +555,39 @@ int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D
     return AMDMOE_OK;
 }
 
+// ------------------------------------------------------- row scales
+// One thread per sorted row: its token's nkb scale dwords (contiguous, read
+// as 16-byte vectors where aligned) go to nkb K-step rows of dst, so each
+// K-step row is written coalesced across the wave.  Rows past the valid
+// ones (sorted_token not written there) read token 0: never consumed.
+__global__ __launch_bounds__(256) void gather_row_scales_kernel(const uint32_t* __restrict__ src,
+                                                                const int* __restrict__ sorted_token,
+                                                                long P, int T, int nkb,
+                                                                uint32_t* __restrict__ dst) {
+    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= P) return;
+    int t = sorted_token[p];
+    t = (t >= 0 && t < T) ? t : 0;
+    const uint32_t* row = src + (size_t)t * nkb;
+    if ((nkb & 3) == 0) {
+        for (int kb = 0; kb < nkb; kb += 4) {
+            const u32x4 v = *(const u32x4*)(row + kb);
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[(size_t)(kb + i) * P + p] = v[i];
+        }
+    } else {
+        for (int kb = 0; kb < nkb; kb++) dst[(size_t)kb * P + p] = row[kb];
+    }
+}
+
+int launch_gather_row_scales(const uint32_t* src, const int* sorted_token, long P, int T, int nkb,
+                             uint32_t* dst, hipStream_t st) {
+    AMDMOE_CHECK_ARG(P >= 0 && T > 0 && nkb > 0, "gather_row_scales: P=%ld T=%d nkb=%d", P, T, nkb);
+    if (P == 0) return AMDMOE_OK;
+    hipLaunchKernelGGL(gather_row_scales_kernel, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, st, src,
+                       sorted_token, P, T, nkb, dst);
+    AMDMOE_LAUNCH_CHECK();
+    return AMDMOE_OK;
+}
+
 }  // namespace amdmoe
