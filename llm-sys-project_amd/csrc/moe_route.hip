@@ -195,6 +195,20 @@ template <> __device__ __forceinline__ float load_f<float>(const float* p) { ret
 template <> __device__ __forceinline__ float load_f<uint16_t>(const uint16_t* p) {
     return bf16_to_f32(*p);
 }
+// eight consecutive elements as fp32 (p 16-byte aligned)
+__device__ __forceinline__ void load8_f(const float* p, float (&v)[8]) {
+    const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = a[i], v[4 + i] = b[i];
+}
+__device__ __forceinline__ void load8_f(const uint16_t* p, float (&v)[8]) {
+    const u32x4 a = *(const u32x4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(a[i] << 16);
+        v[2 * i + 1] = __uint_as_float(a[i] & 0xffff0000u);
+    }
+}
 
 // ---------------------------------------------------------------- exact
 // Block = 256 threads = 4 waves.  tpb tokens per block (tpb*E <= 256 when
@@ -204,7 +218,7 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
                                                           const GT* __restrict__ wg,
                                                           const float* __restrict__ bias, int T,
                                                           int E, int K, int D, int tpb,
-                                                          int* __restrict__ idx,
+                                                          bool vec, int* __restrict__ idx,
                                                           float* __restrict__ wts) {
     extern __shared__ float s_logit[];  // [tpb][E]
     const int tid = threadIdx.x;
@@ -217,7 +231,21 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
         if (t < T) {
             const XT* xr = x + (size_t)t * D;
             const GT* wr = wg + (size_t)e * D;
-            for (int d = 0; d < D; d++) sum = mac_rn(sum, load_f(xr + d), load_f(wr + d));
+            // the reference's order (d ascending, multiply then add); the
+            // operands arrive eight at a time (16-byte loads) when the rows
+            // are 16-byte aligned -- the dependent adds, not the loads, are
+            // then the critical path
+            int d = 0;
+            if (vec) {
+                for (; d + 8 <= D; d += 8) {
+                    float xv[8], wv[8];
+                    load8_f(xr + d, xv);
+                    load8_f(wr + d, wv);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sum = mac_rn(sum, xv[i], wv[i]);
+                }
+            }
+            for (; d < D; d++) sum = mac_rn(sum, load_f(xr + d), load_f(wr + d));
             if (bias) sum = add_rn(sum, bias[e]);
         }
         s_logit[j] = sum;
@@ -458,8 +486,11 @@ int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int 
     size_t lds = sizeof(float) * (size_t)tpb * E;
     AMDMOE_CHECK_ARG(lds <= 64 * 1024, "routing: E=%d too large for the exact gate", E);
     int grid = (int)ceil_div(T, tpb);
+    // every row 16-byte aligned: base pointers aligned, rows a multiple of 16 bytes
+    const bool vec = ((uintptr_t)x & 15) == 0 && ((uintptr_t)wg & 15) == 0 && (D * sizeof(XT)) % 16 == 0 &&
+                     (D * sizeof(GT)) % 16 == 0;
     hipLaunchKernelGGL((route_exact_kernel<XT, GT>), dim3(grid), dim3(256), lds, st, x, wg, bias,
-                       T, E, K, D, tpb, idx, wts);
+                       T, E, K, D, tpb, vec, idx, wts);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
