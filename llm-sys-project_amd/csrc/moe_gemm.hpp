@@ -70,7 +70,7 @@ constexpr int kRbSmall = 4, kRbLarge = 3;
 // activations through registers (global -> VGPR -> ds_write) instead of the
 // LDS DMA: measured cheaper per byte, and the registers are there while the
 // accumulators are few
-constexpr int kVgMaxR = 10;
+constexpr int kVgMaxR = 12;
 constexpr int kEpiPitch = 132;                         // floats per staged output row
 constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
 constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
