@@ -85,6 +85,15 @@ __device__ __forceinline__ uint32_t f32x4_to_e4m3x4(float a, float b, float c, f
     return (uint32_t)v;
 }
 
+// The same conversion for inputs known to lie within +-448 up to rounding
+// (RNE takes anything below 464 to at most 448).
+__device__ __forceinline__ uint32_t f32x4_to_e4m3x4_noclamp(float a, float b, float c, float d) {
+    int v = 0;
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, v, false);
+    v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
+    return (uint32_t)v;
+}
+
 // ------------------------------------------------------------------ MFMA
 // 16x16 output tiles.  Operand lane layout (A and B alike): lane l supplies
 // row/column (l & 15) and the K-slot group (l >> 4).  Output: lane l holds

@@ -71,6 +71,8 @@ constexpr int kRbSmall = 4, kRbLarge = 3;
 // LDS DMA: measured cheaper per byte, and the registers are there while the
 // accumulators are few
 constexpr int kVgMaxR = 12;
+constexpr float kNegLog2e = -1.4426950408889634f;  // -log2(e)
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kEpiPitch = 132;                         // floats per staged output row
 constexpr int kEpiRows = 128;                          // epilogue stages 128 rows at a time
 constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [256] weight
@@ -409,7 +411,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         if (DT == DT_FP8) {
             const float* sbs = (const float*)(smem + kBScaleOff);
             const int kb = kblk(kt);
-            if (MODE == MODE_UP) { sb0 = sbs[kb]; sb1 = sbs[kMaxKb + kb]; }
+            // UP: the gate rows accumulate -log2(e) * g (the exponent the
+            // epilogue's exp2 takes), folded into their block scale here
+            if (MODE == MODE_UP) { sb0 = sbs[kb] * kNegLog2e; sb1 = sbs[kMaxKb + kb]; }
             else { sb0 = sb1 = sbs[(wave >> 2) * kMaxKb + kb]; }
         }
         auto load_x = [&](int rt, i32x8& xv, float& sx) __attribute__((always_inline)) {
@@ -698,12 +702,18 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 f32x4 hv;
                 for (int i = 0; i < 4; i++) {
                     const float gv = acc[rt][0][i], uv = acc[rt][1][i];
-                    // fp32 keeps the reference's expf and IEEE division
-                    // (naive_moe.cu:297-310); the bf16 / fp8 epilogues use
-                    // the hardware exp2 and reciprocal (~1 ulp each)
-                    const float silu = DT == DT_F32 ? gv / (1.0f + expf(-gv))
-                                                    : gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
-                    hv[i] = silu * uv;
+                    if constexpr (DT == DT_FP8) {
+                        // gv = -log2(e) g: h' = gv u / (1 + 2^gv) = -log2(e) h
+                        // (the quantisation below takes the constant back)
+                        hv[i] = gv * uv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gv));
+                    } else {
+                        // fp32 keeps the reference's expf and IEEE division
+                        // (naive_moe.cu:297-310); bf16 / MX use the hardware
+                        // exp2 and reciprocal (~1 ulp each)
+                        const float silu = DT == DT_F32 ? gv / (1.0f + expf(-gv))
+                                                        : gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
+                        hv[i] = silu * uv;
+                    }
                 }
                 *(f32x4*)&Tb[(16 * r8 + r16) * kEpiPitch + 16 * wave + 4 * q] = hv;
             }
@@ -721,22 +731,27 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
             const size_t pos = (size_t)row0 + rr;
             if (DT == DT_FP8) {
+                // the staged values are h' = -log2(e) h: amax(h) = ln2 amax(h'),
+                // and h * inv = h' * (-ln2 inv)
                 float amax = 0.0f;
                 for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
                 amax = fmaxf(amax, __shfl_xor(amax, 1, kWave));
                 amax = fmaxf(amax, __shfl_xor(amax, 2, kWave));
+                amax *= kLn2;
                 const float s = amax > 0.0f ? __fdiv_rn(amax, 448.0f) : 1.0f;
-                // q = v * (1/s): one correctly rounded reciprocal per block
-                // instead of 32 divisions (codes may differ from v / s by one
-                // step where v / s lies within an ulp of an e4m3 midpoint)
-                const float inv = __fdiv_rn(1.0f, s);
+                // q = h * (1/s): one correctly rounded reciprocal per block
+                // instead of 32 divisions (codes may differ from h / s by one
+                // step where h / s lies within an ulp of an e4m3 midpoint);
+                // |h / s| <= 448 up to rounding, which RNE takes to 448, so the
+                // conversion needs no clamp
+                const float inv = -kLn2 * __fdiv_rn(1.0f, s);
                 if (ok) {
                     u32x4 o0, o1;
                     for (int k = 0; k < 4; k++) {
-                        o0[k] = f32x4_to_e4m3x4(v[4 * k] * inv, v[4 * k + 1] * inv,
-                                                v[4 * k + 2] * inv, v[4 * k + 3] * inv);
-                        o1[k] = f32x4_to_e4m3x4(v[16 + 4 * k] * inv, v[16 + 4 * k + 1] * inv,
-                                                v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
+                        o0[k] = f32x4_to_e4m3x4_noclamp(v[4 * k] * inv, v[4 * k + 1] * inv,
+                                                        v[4 * k + 2] * inv, v[4 * k + 3] * inv);
+                        o1[k] = f32x4_to_e4m3x4_noclamp(v[16 + 4 * k] * inv, v[16 + 4 * k + 1] * inv,
+                                                        v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
                     }
                     uint8_t* dst = g.out + pos * g.n_out + col;
                     *(u32x4*)dst = o0;
