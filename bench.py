@@ -565,17 +565,24 @@ def main():
     torch.cuda.synchronize()
 
     def timed(forward):
-        stage = [amdmoe.StageEvents() for _ in range(args.steps)]
+        # the step time comes from a pass without stage events (their seven
+        # event records per step are instrumentation, not the layer); the
+        # stage times from a second pass of the same length with them
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0.record()
         for i in range(args.steps):
-            stage[i].arm()
             forward()
         t1.record()
-        amdmoe.StageEvents.disarm()
         torch.cuda.synchronize()
         ms = t0.elapsed_time(t1) / args.steps
+        stage = [amdmoe.StageEvents() for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            stage[i].arm()
+            forward()
+        amdmoe.StageEvents.disarm()
+        torch.cuda.synchronize()
         per_stage = {n: sum(s.stage_ms()[n] for s in stage) / args.steps for n in amdmoe.StageEvents.NAMES}
         log(f"[bench] {ms:.4f} ms/step; stage ms: " + ", ".join(f"{k}={v:.4f}" for k, v in per_stage.items()))
         return ms, per_stage
