@@ -71,6 +71,7 @@ constexpr int kRbSmall = 4, kRbLarge = 3;
 // LDS DMA: measured cheaper per byte, and the registers are there while the
 // accumulators are few
 constexpr int kVgMaxR = 12;
+constexpr int kVgMaxRMx = 0;   // MX: none (its fragments hold scale registers too; the register path spilled)
 constexpr float kNegLog2e = -1.4426950408889634f;  // -log2(e)
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kEpiPitch = 132;                         // floats per staged output row
@@ -112,8 +113,14 @@ __device__ __forceinline__ void pin(BFragMx& f) {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void pin3(u32x4 (&a)[3]) {
-    asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]));
+// the first N registers of a register-path activation set
+template <int N>
+__device__ __forceinline__ void pin_av(u32x4 (&a)[4]) {
+    static_assert(N >= 1 && N <= 4, "one to four slabs");
+    asm volatile("" : "+v"(a[0]));
+    if constexpr (N > 1) asm volatile("" : "+v"(a[1]));
+    if constexpr (N > 2) asm volatile("" : "+v"(a[2]));
+    if constexpr (N > 3) asm volatile("" : "+v"(a[3]));
 }
 
 // 16-byte buffer load into registers, issued as inline asm so the compiler
@@ -360,13 +367,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     uint8_t* const st_ = smem + ((KT_A) % kNS) * kStageBytes
     auto issue_slot = [&](auto rc, int sl, __amdgpu_buffer_rsrc_t ra_, __amdgpu_buffer_rsrc_t rs_,
                           i32x4 rb_, i32x4 rbs_, i32x4 rv_, int so_a, int so_s, int so_b, int so_bs,
-                          int so_v, uint8_t* st_, Frag& f, u32x4 (&av)[3]) __attribute__((always_inline)) {
+                          int so_v, uint8_t* st_, Frag& f, u32x4 (&av)[4]) __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;
         constexpr int NS = (R + 3) / 4;
         constexpr int kAS = NS + (kScaledA ? 1 : 0);
         if (sl < NS) {
-            if constexpr (kScaledA && R <= kVgMaxR)  // register path: K-step KT_V into av
-                av[sl < 3 ? sl : 0] = buffer_load_b128_async<0>(rv_, voff_a[sl], so_v);
+            if constexpr ((kScaledA && R <= (DT == DT_MX ? kVgMaxRMx : kVgMaxR)) || (DT == DT_FP8 && R > kVgMaxR))  // register path: K-step KT_V into av
+                av[sl < 4 ? sl : 0] = buffer_load_b128_async<0>(rv_, voff_a[sl], so_v);
             else
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     ra_, (lds_ptr_t)(st_ + (64 * sl + 8 * wave) * 128), 16, voff_a[sl], so_a, 0, 0);
@@ -528,13 +535,14 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // step's loads at once parks every wave at the issue for most of the
     // step.  Slot s goes out right after the MFMAs of token tile
     // (s * tiles) / kSl, so the activation slots go first.
-    auto step = [&](auto stc, auto rc, auto rbc, int kt, Frag& cur, Frag& refill, u32x4 (&av_w)[3],
-                    u32x4 (&av_l)[3]) __attribute__((always_inline)) {
+    auto step = [&](auto stc, auto rc, auto rbc, int kt, Frag& cur, Frag& refill, u32x4 (&av_w)[4],
+                    u32x4 (&av_l)[4]) __attribute__((always_inline)) {
         constexpr int R = decltype(rc)::value;  // token tiles per step
         constexpr int RB = decltype(rbc)::value;
         constexpr int NS = (R + 3) / 4;
         constexpr int kSl = NS + (kScaledA ? 1 : 0) + 4;
-        constexpr bool kVg = kScaledA && R <= kVgMaxR;
+        constexpr bool kVg = kScaledA && R <= (DT == DT_MX ? kVgMaxRMx : kVgMaxR);
+        constexpr bool kVg1 = DT == DT_FP8 && R > kVgMaxR;  // one register set (MX: registers run out)
         // Issue order per step: activation slots of step kt+2, then the 4
         // weight loads of step kt+RB-1.  Everything of step kt has landed
         // once at most kWait vector-memory instructions are outstanding:
@@ -556,23 +564,30 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         //            kt the activations of step kt+1 (issued at step kt-2) are
         //            written to LDS, so at most the NS + 5 loads of step kt-1
         //            and the 4 weight loads of step kt-2 may be outstanding.
+        //   register path with one set (kVg1, RB == 3): per step the
+        //            activations of step kt+2 (registers), the scale slot of
+        //            step kt+2, the weights of step kt+2.  At the top of step
+        //            kt the activations of step kt+1 (issued at step kt-1, the
+        //            step's oldest loads) are written to LDS: only the scale
+        //            and the 4 weight loads of step kt-1 may be outstanding.
         static_assert(RB >= 2 && RB <= 5, "wait counts are derived for rings of 2 to 5 sets");
         static_assert(!kVg || RB == 4, "the register path's wait count is derived for RB == 4");
-        wait_vmcnt<kVg ? NS + 9 : (RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0)))>();
+        static_assert(!kVg1 || RB == 3, "the one-set register path's wait count is derived for RB == 3");
+        wait_vmcnt<kVg ? NS + 9 : (kVg1 ? 5 : (RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0))))>();
         // the weights of this step have landed: pin every use of them below
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
-        if constexpr (kVg) {
+        if constexpr (kVg || kVg1) {
             // activations of step kt+1 -> LDS stage (kt+1) % 3, the slab
             // layout the DMA would give (lane l's 16 bytes at 16 l); that
             // stage was last read at step kt-2, which every wave has left
-            pin3(av_w);
+            pin_av<NS>(av_w);
             uint8_t* stw = smem + ((kt + 1) % kNS) * kStageBytes + 8 * wave * 128 + 16 * lane;
 #pragma unroll
             for (int sl = 0; sl < NS; sl++) *(u32x4*)(stw + 64 * sl * 128) = av_w[sl];
         }
         bare_barrier();
-        STEP_ADDR(kt + 2, kt + RB - 1, kt + 3);
+        STEP_ADDR(kt + 2, kt + RB - 1, kt + (kVg1 ? 2 : 3));
         auto tile_issued = [&](int rt) __attribute__((always_inline)) {
             for (int sl = 0; sl < kSl; sl++)
                 if ((sl * R) / kSl == rt) issue_slot(rc, sl, SLOT_ARGS, refill, av_l);
@@ -593,9 +608,32 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             for (int j = 0; j < 2; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
         Frag bs[RB];
         constexpr int NS = (R + 3) / 4;
-        constexpr bool kVg = kScaledA && R <= kVgMaxR;
-        u32x4 av[2][3];  // register path: activations of odd / even K-steps
-        if constexpr (kVg) {
+        constexpr bool kVg = kScaledA && R <= (DT == DT_MX ? kVgMaxRMx : kVgMaxR);
+        constexpr bool kVg1 = DT == DT_FP8 && R > kVgMaxR;
+        u32x4 av[2][4];  // register path: activations of odd / even K-steps (kVg1: set 0 only)
+        if constexpr (kVg1) {
+            // prologue of the one-set register path: activations, scale and
+            // weights of step 0; the activations -> LDS stage 0 once landed
+            // (the scale and weight loads may be outstanding); then those of
+            // step 1.  Step j then issues the activations, scale and weights
+            // of step j+2.
+            {
+                STEP_ADDR(0, 0, 0);
+                for (int sl = 0; sl < NS + 5; sl++) issue_slot(rc, sl, SLOT_ARGS, bs[0], av[0]);
+            }
+            wait_vmcnt<5>();
+            pin_av<NS>(av[0]);
+            {
+                uint8_t* stw = smem + 8 * wave * 128 + 16 * lane;
+#pragma unroll
+                for (int sl = 0; sl < NS; sl++) *(u32x4*)(stw + 64 * sl * 128) = av[0][sl];
+            }
+            {
+                STEP_ADDR(1, 1, 1);
+                for (int sl = 0; sl < NS + 5; sl++) issue_slot(rc, sl, SLOT_ARGS, bs[1], av[0]);
+            }
+            lds_wait();  // stage 0 written before step 0's barrier
+        } else if constexpr (kVg) {
             // prologue of the register path: groups (activations, scale,
             // weights) of steps 0 and 1; the activations of step 0 -> LDS
             // stage 0 once landed (the NS + 10 newer loads may be
@@ -608,7 +646,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 for (int sl = 0; sl < NS + 5; sl++) issue_slot(rc, sl, SLOT_ARGS, bs[i], av[i]);
             });
             wait_vmcnt<NS + 10>();
-            pin3(av[0]);
+            pin_av<NS>(av[0]);
             {
                 uint8_t* stw = smem + 8 * wave * 128 + 16 * lane;
 #pragma unroll
@@ -641,21 +679,23 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         for (; kt + RB <= nk; kt += RB) {
             static_for<RB>([&](auto stc) __attribute__((always_inline)) {
                 constexpr int ST = decltype(stc)::value;
-                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[(ST + 1) & 1], av[(ST + 1) & 1]);
+                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[kVg1 ? 0 : (ST + 1) & 1],
+                     av[kVg1 ? 0 : (ST + 1) & 1]);
             });
         }
         static_for<RB - 1>([&](auto stc) __attribute__((always_inline)) {
             constexpr int ST = decltype(stc)::value;
             if (kt + ST < nk)
-                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[(ST + 1) & 1], av[(ST + 1) & 1]);
+                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[kVg1 ? 0 : (ST + 1) & 1],
+                     av[kVg1 ? 0 : (ST + 1) & 1]);
         });
         // drain the trailing (out-of-range) prefetches before the ring and
         // the weight registers are reused
         wait_vmcnt<0>();
         static_for<RB>([&](auto ic) __attribute__((always_inline)) { pin(bs[decltype(ic)::value]); });
-        if constexpr (kVg) {
-            pin3(av[0]);
-            pin3(av[1]);
+        if constexpr (kVg || kVg1) {
+            pin_av<NS>(av[0]);
+            if constexpr (kVg) pin_av<NS>(av[1]);
         }
 #pragma unroll
         for (int i = R; i < 16; i++)
