@@ -324,7 +324,7 @@ def kernel_label(name):
     base = name.split("(")[0].replace("void ", "").replace("amdmoe::", "").strip()
     m = re.match(r"grouped_gemm_kernel<(\d), (\d), (true|false)>", base)
     if m:
-        dt = ("f32", "bf16", "fp8")[int(m.group(1))]
+        dt = ("f32", "bf16", "fp8", "MX")[int(m.group(1))]
         mode = ("UP", "DOWN")[int(m.group(2))]
         lay = "packed" if m.group(3) == "true" else "row-major"
         return f"grouped_gemm_kernel<{dt}, {mode}, {lay}>"
