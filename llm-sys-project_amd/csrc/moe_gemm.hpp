@@ -683,12 +683,20 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                      av[kVg1 ? 0 : (ST + 1) & 1]);
             });
         }
-        static_for<RB - 1>([&](auto stc) __attribute__((always_inline)) {
+        // the tail, nested: tail step ST runs only after tail step ST-1 (no
+        // control-flow path reaches a step without the loads of the one
+        // before it)
+        auto tail = [&](auto self, auto stc) __attribute__((always_inline)) {
             constexpr int ST = decltype(stc)::value;
-            if (kt + ST < nk)
-                step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[kVg1 ? 0 : (ST + 1) & 1],
-                     av[kVg1 ? 0 : (ST + 1) & 1]);
-        });
+            if constexpr (ST < RB - 1) {
+                if (kt + ST < nk) {
+                    step(stc, rc, rbc, kt + ST, bs[ST], bs[(ST + RB - 1) % RB], av[kVg1 ? 0 : (ST + 1) & 1],
+                         av[kVg1 ? 0 : (ST + 1) & 1]);
+                    self(self, std::integral_constant<int, ST + 1>());
+                }
+            }
+        };
+        tail(tail, std::integral_constant<int, 0>());
         // drain the trailing (out-of-range) prefetches before the ring and
         // the weight registers are reused
         wait_vmcnt<0>();

@@ -6,9 +6,9 @@ The weight loads of grouped_gemm_kernel are inline-asm
 know they are still in flight, so nothing may read or overwrite their
 destination registers until an explicit `s_waitcnt vmcnt(...)`.  This walks
 every control-flow path from each such load (following branches) to the
-first vmcnt wait and reports any instruction on the way that names one of
-the destination registers -- a copy, a spill, an MFMA reading it too early,
-or a reuse of the register.
+first vmcnt wait that covers it and reports any instruction on the way that
+names one of the destination registers -- a copy, a spill, an MFMA reading
+it too early, or a reuse of the register.
 """
 import re
 
@@ -21,8 +21,18 @@ def _regs(tok):
     return {int(m.group(1))} if m else set()
 
 
+_VMEM = ("buffer_", "global_", "flat_", "scratch_", "tbuffer_")
+_VMCNT = re.compile(r"vmcnt\((\d+)\)")
+
+
 def violations(asm_text):
-    """[(kernel, line, instruction)] for every hazard found."""
+    """[(kernel, line, instruction)] for every hazard found.
+
+    vmcnt counts vector-memory instructions (loads, stores and LDS DMA alike
+    on gfx9) and they complete in issue order, so `s_waitcnt vmcnt(N)` has
+    landed a load once at least N vector-memory instructions were issued
+    after it on the path walked; a wait with a larger N does not end the
+    walk."""
     lines = [ln.split(";")[0].strip() for ln in asm_text.split("\n")]
     labels = {}
     for i, ln in enumerate(lines):
@@ -38,28 +48,34 @@ def violations(asm_text):
         if not m or ln.endswith(" lds"):
             continue
         dst = _regs(m.group(1))
-        stack, seen = [i + 1], set()
-        while stack:
-            j = stack.pop()
-            while j < len(lines) and j not in seen:
-                seen.add(j)
+        stack, seen, found = [(i + 1, 0)], set(), False
+        while stack and not found:
+            j, k = stack.pop()
+            while j < len(lines) and (j, k) not in seen:
+                seen.add((j, k))
                 t = lines[j]
-                if t.startswith("s_waitcnt") and "vmcnt" in t:
-                    break
+                if t.startswith("s_waitcnt"):
+                    w = _VMCNT.search(t)
+                    if w and int(w.group(1)) <= k:
+                        break
                 if t.startswith("s_endpgm"):
                     bad.append((kern, i + 1, "reaches s_endpgm with the load in flight"))
+                    found = True
                     break
                 if t.startswith("s_branch"):
                     j = labels[t.split()[1]]
                     continue
                 if t.startswith("s_cbranch"):
-                    stack.append(labels[t.split()[1]])
-                if t and not t.endswith(":") and not t.startswith(".") \
-                        and not t.startswith("buffer_load_dwordx4") and not t.startswith("buffer_load_ubyte"):
-                    ops = re.split(r"[ ,]+", t)[1:]
-                    if set().union(set(), *[_regs(o) for o in ops]) & dst:
-                        bad.append((kern, j + 1, t))
-                        break
+                    stack.append((labels[t.split()[1]], k))
+                if t and not t.endswith(":") and not t.startswith("."):
+                    if not (t.startswith("buffer_load_dwordx4") or t.startswith("buffer_load_ubyte")):
+                        ops = re.split(r"[ ,]+", t)[1:]
+                        if set().union(set(), *[_regs(o) for o in ops]) & dst:
+                            bad.append((kern, j + 1, t))
+                            found = True
+                            break
+                    if t.startswith(_VMEM):
+                        k = min(k + 1, 64)
                 j += 1
     return bad
 

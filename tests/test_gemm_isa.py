@@ -25,6 +25,17 @@ def test_checker_flags_a_copy_before_the_wait():
     assert violations(clean) == []
 
 
+def test_checker_counts_newer_loads_before_a_wait_covers():
+    # vmcnt(1) leaves the newest load in flight: it covers the first load
+    # only when another vector-memory instruction was issued after it
+    asm = "\n".join([
+        "_Zk:", "\tbuffer_load_dwordx4 v[2:5], v1, s[0:3], s4 offen offset:0",
+        "\ts_waitcnt vmcnt(1)", "\tv_mov_b32_e32 v9, v3", "\ts_waitcnt vmcnt(0)", "\ts_endpgm"])
+    assert len(violations(asm)) == 1
+    covered = asm.replace("offset:0\n", "offset:0\n\tglobal_store_dword v1, v6, s[6:7]\n")
+    assert violations(covered) == []
+
+
 def test_sgpr_checker_flags_a_valu_written_soffset():
     asm = "\n".join([
         "_Zk:", "\tv_readfirstlane_b32 s4, v3",
