@@ -195,9 +195,12 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     const long mtiles = max_mtiles(P, E);
     const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);  // activation bytes per element
     const int wdiv = dt == DT_MX ? 2 : 1;                       // MX weights: two E2M1 per byte
+    // fp8 / MX: with the permutation, x's block scales K-step major in
+    // sorted row order (the grouped GEMM's a_scale layout)
     TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
                        w.sorted_slot, w.tiles, w.num_tiles,
-                       permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st));
+                       permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st,
+                       (const uint32_t*)x_scale, x_scale ? D / 128 : 0, x_scale ? (uint32_t*)w.xs_sorted : nullptr));
     TRY(mark(3, st));
     if (dt == DT_F32 && !f32_mfma_shape(c)) {
         TRY(launch_experts_f32_any((const float*)a_x, (const float*)w1, (const float*)w2, T, E, K,
@@ -208,10 +211,6 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
         TRY(mark(5, st));
         return mark(6, st);
     }
-    // fp8 / MX: the activation scales K-step major in sorted row order
-    if (x_scale)
-        TRY(launch_gather_row_scales((const uint32_t*)x_scale, w.sorted_token, P, T, D / 128,
-                                     (uint32_t*)w.xs_sorted, st));
     GemmArgs up{};
     up.a = a_x;
     up.a_bytes = (long)T * D * es;

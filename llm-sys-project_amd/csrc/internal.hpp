@@ -65,9 +65,13 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
 // kernel); permute_scratch_bytes returns 0 where only the latter applies
 size_t permute_scratch_bytes(int T, int E);
 // wts / sorted_w: optional (both or neither): sorted_w[row] = wts[slot of row]
+// rs_src / rs_dst: optional (both or neither): the row scales of
+// launch_gather_row_scales (rs_nkb per token) in sorted row order, fused
+// into the decode-sized single-launch permutation
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   int* scratch, const float* wts, float* sorted_w, hipStream_t st);
+                   int* scratch, const float* wts, float* sorted_w, hipStream_t st,
+                   const uint32_t* rs_src = nullptr, int rs_nkb = 0, uint32_t* rs_dst = nullptr);
 int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D, int expert,
                       float* gathered, int* token_map, int* count, hipStream_t st);
 

@@ -413,13 +413,16 @@ __global__ __launch_bounds__(kSmallSlots) void perm_small_kernel(
     const int* __restrict__ idx, int T, int K, int E, int BM, int* __restrict__ counts,
     int* __restrict__ offsets, int4* __restrict__ tiles, int* __restrict__ num_tiles,
     int* __restrict__ sorted_token, int* __restrict__ sorted_slot, const float* __restrict__ wts,
-    float* __restrict__ sorted_w) {
+    float* __restrict__ sorted_w, const uint32_t* __restrict__ rs_src, int rs_nkb,
+    uint32_t* __restrict__ rs_dst) {
     constexpr int kWaves = kSmallSlots / 64;
     __shared__ unsigned long long s_mask[kWaves][kSmallMaxE];
     __shared__ int s_off[kSmallMaxE];
     __shared__ int s_wr[kWaves], s_wt[kWaves];
+    __shared__ int s_tok[kSmallSlots];  // token of each sorted row (row scales)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int i = tid; i < kWaves * kSmallMaxE; i += kSmallSlots) (&s_mask[0][0])[i] = 0ull;
+    s_tok[tid] = 0;
     __syncthreads();
     const int e = tid < T * K ? slot_expert(idx, tid, K, E) : -1;
     if (e >= 0) atomicOr(&s_mask[wave][e], 1ull << lane);
@@ -461,6 +464,29 @@ __global__ __launch_bounds__(kSmallSlots) void perm_small_kernel(
         sorted_token[pos] = tid / K;
         sorted_slot[pos] = tid;
         if (sorted_w) sorted_w[pos] = wts[tid];
+        s_tok[pos] = tid / K;
+    }
+    if (rs_dst) {
+        // the row scales (gather_row_scales_kernel's contract): work unit j =
+        // (4-dword chunk c, row p), rows fastest, so each K-step row of
+        // rs_dst is written coalesced and every thread has one 16-byte load
+        // in flight per round (4-byte loads if a token's row is not 16-byte
+        // aligned)
+        __syncthreads();
+        const int P = T * K;
+        const int nc = (rs_nkb + 3) >> 2;
+        const bool vec = (rs_nkb & 3) == 0;
+        for (int j = tid; j < nc * P; j += kSmallSlots) {
+            const int c = j / P, p = j - c * P;
+            const uint32_t* row = rs_src + (size_t)s_tok[p] * rs_nkb + 4 * c;
+            if (vec) {
+                const u32x4 v = *(const u32x4*)row;
+#pragma unroll
+                for (int i = 0; i < 4; i++) rs_dst[(size_t)(4 * c + i) * P + p] = v[i];
+            } else {
+                for (int i = 0; i < 4 && 4 * c + i < rs_nkb; i++) rs_dst[(size_t)(4 * c + i) * P + p] = row[i];
+            }
+        }
     }
 }
 
@@ -470,15 +496,31 @@ size_t permute_scratch_bytes(int T, int E) {
     return (size_t)(2 * nblk * E) * sizeof(int);
 }
 
+int launch_gather_row_scales(const uint32_t* src, const int* sorted_token, long P, int T, int nkb,
+                             uint32_t* dst, hipStream_t st);
+
 int launch_permute(const int* idx, int T, int K, int E, int BM, int* counts, int* offsets,
                    int* sorted_token, int* sorted_slot, int4* tiles, int* num_tiles,
-                   int* scratch, const float* wts, float* sorted_w, hipStream_t st) {
+                   int* scratch, const float* wts, float* sorted_w, hipStream_t st,
+                   const uint32_t* rs_src, int rs_nkb, uint32_t* rs_dst) {
     AMDMOE_CHECK_ARG((wts == nullptr) == (sorted_w == nullptr), "permute: wts and sorted_w go together");
+    AMDMOE_CHECK_ARG((rs_src == nullptr) == (rs_dst == nullptr) && (!rs_dst || rs_nkb > 0),
+                     "permute: rs_src and rs_dst go together (nkb=%d)", rs_nkb);
     if (T > 0 && (long)T * K <= kSmallSlots && E <= kSmallMaxE) {
+        // decode-sized: one launch, the row scales included
         hipLaunchKernelGGL(perm_small_kernel, dim3(1), dim3(kSmallSlots), 0, st, idx, T, K, E, BM, counts,
-                           offsets, tiles, num_tiles, sorted_token, sorted_slot, wts, sorted_w);
+                           offsets, tiles, num_tiles, sorted_token, sorted_slot, wts, sorted_w, rs_src,
+                           rs_nkb, rs_dst);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
+    }
+    if (rs_dst) {
+        // the multi-block scatters write scattered rows: gather the scales
+        // after them in a launch of their own (coalesced writes)
+        const int rc = launch_permute(idx, T, K, E, BM, counts, offsets, sorted_token, sorted_slot, tiles,
+                                      num_tiles, scratch, wts, sorted_w, st, nullptr, 0, nullptr);
+        if (rc != AMDMOE_OK) return rc;
+        return launch_gather_row_scales(rs_src, sorted_token, (long)T * K, T, rs_nkb, rs_dst, st);
     }
     if (scratch && T > 0 && permute_scratch_bytes(T, E) > 0) {
         const int nblk = (T + kPermTok - 1) / kPermTok;
