@@ -71,6 +71,28 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
+// v / s rounded to nearest, for values that share the divisor s (a block
+// scale): one correctly rounded reciprocal r = RN(1/s) per block, then per
+// value q0 = RN(v r) and one FMA correction, RN(q0 + RN(v - s q0) r).  By
+// Markstein's theorem (r within half an ulp of 1/s, q0 within one ulp of
+// v/s, so v - s q0 is exact under an FMA) the result is the correctly
+// rounded quotient, the same value as an IEEE division.  The identity needs
+// r, q0 and the residual in the normal range, which holds for s >= 2^-64
+// and every quotient that does not round to zero in e4m3; smaller scales
+// take the IEEE division.
+struct BlockDivisor {
+    float s, r;
+    bool fast;
+};
+__device__ __forceinline__ BlockDivisor block_divisor(float s) {
+    return {s, __fdiv_rn(1.0f, s), s >= 0x1p-64f};
+}
+__device__ __forceinline__ float div_rn(const BlockDivisor& d, float v) {
+    if (!d.fast) return __fdiv_rn(v, d.s);
+    const float q0 = v * d.r;
+    return __builtin_fmaf(__builtin_fmaf(-q0, d.s, v), d.r, q0);
+}
+
 // Four floats -> four OCP e4m3 bytes (RNE).  Inputs are pre-clamped to
 // +-448 so the hardware conversion never sees an out-of-range value; the
 // result then equals round-to-nearest-even with saturation.

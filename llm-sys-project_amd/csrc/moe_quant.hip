@@ -4,8 +4,9 @@
 //   activations: one fp32 scale per row per 128 columns, scale = amax/448,
 //                q = e4m3_rne_sat(v / scale)  (scale 1 for an all-zero block)
 //   weights:     one fp32 scale per 128x128 block, scale = u*amax/448.
-// The divisions are IEEE round-to-nearest (__fdiv_rn) so the codes are
-// bit-identical to the oracle's.
+// The divisions are IEEE round-to-nearest (__fdiv_rn; for the activations
+// div_rn, whose reciprocal and FMA correction give the same quotients), so
+// the codes are bit-identical to the oracle's.
 #include "internal.hpp"
 
 namespace amdmoe {
@@ -56,9 +57,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
             am = dpp_max<0x140>(dpp_max<0x141>(dpp_max<0x4E>(dpp_max<0xB1>(am))));
             if (col >= cols) continue;  // the whole 16-lane block is past the row
             const float sc = am > 0.0f ? __fdiv_rn(am, 448.0f) : 1.0f;
+            const BlockDivisor d = block_divisor(sc);
             u32x2 c;
-            c[0] = f32x4_to_e4m3x4(__fdiv_rn(f[0], sc), __fdiv_rn(f[1], sc), __fdiv_rn(f[2], sc), __fdiv_rn(f[3], sc));
-            c[1] = f32x4_to_e4m3x4(__fdiv_rn(f[4], sc), __fdiv_rn(f[5], sc), __fdiv_rn(f[6], sc), __fdiv_rn(f[7], sc));
+            c[0] = f32x4_to_e4m3x4(div_rn(d, f[0]), div_rn(d, f[1]), div_rn(d, f[2]), div_rn(d, f[3]));
+            c[1] = f32x4_to_e4m3x4(div_rn(d, f[4]), div_rn(d, f[5]), div_rn(d, f[6]), div_rn(d, f[7]));
             *(u32x2*)(qr + col) = c;
             if ((lane & 15) == 0) scale[r * nb + col / 128] = sc;
         }

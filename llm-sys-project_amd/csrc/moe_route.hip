@@ -421,13 +421,14 @@ __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __res
             } else if (qtok < T) {
                 am = fmaxf(am, qam);
                 const float sc = am > 0.0f ? __fdiv_rn(am, 448.0f) : 1.0f;
+                const BlockDivisor dv = block_divisor(sc);
                 const int blk = kg >> 1;
                 uint8_t* dst = xq + (size_t)qtok * D + blk * 128 + 8 * qc;
                 u32x2 c0, c1;
-                c0[0] = f32x4_to_e4m3x4(__fdiv_rn(qv[0], sc), __fdiv_rn(qv[1], sc), __fdiv_rn(qv[2], sc), __fdiv_rn(qv[3], sc));
-                c0[1] = f32x4_to_e4m3x4(__fdiv_rn(qv[4], sc), __fdiv_rn(qv[5], sc), __fdiv_rn(qv[6], sc), __fdiv_rn(qv[7], sc));
-                c1[0] = f32x4_to_e4m3x4(__fdiv_rn(f[0], sc), __fdiv_rn(f[1], sc), __fdiv_rn(f[2], sc), __fdiv_rn(f[3], sc));
-                c1[1] = f32x4_to_e4m3x4(__fdiv_rn(f[4], sc), __fdiv_rn(f[5], sc), __fdiv_rn(f[6], sc), __fdiv_rn(f[7], sc));
+                c0[0] = f32x4_to_e4m3x4(div_rn(dv, qv[0]), div_rn(dv, qv[1]), div_rn(dv, qv[2]), div_rn(dv, qv[3]));
+                c0[1] = f32x4_to_e4m3x4(div_rn(dv, qv[4]), div_rn(dv, qv[5]), div_rn(dv, qv[6]), div_rn(dv, qv[7]));
+                c1[0] = f32x4_to_e4m3x4(div_rn(dv, f[0]), div_rn(dv, f[1]), div_rn(dv, f[2]), div_rn(dv, f[3]));
+                c1[1] = f32x4_to_e4m3x4(div_rn(dv, f[4]), div_rn(dv, f[5]), div_rn(dv, f[6]), div_rn(dv, f[7]));
                 *(u32x2*)dst = c0;
                 *(u32x2*)(dst + 64) = c1;
                 if (qc == 0) xs[(size_t)qtok * (D / 128) + blk] = sc;

@@ -48,6 +48,8 @@ def test_quant_rows_bit_exact(amd, orc, cols):
     x[3, :128] = 0.0
     x[5, -128:] *= np.float32(1e-5)                       # subnormal e4m3 codes
     x[7, cols // 256 * 128:][:128] = np.float32(1.0)      # constant block
+    x[9, :128] *= np.float32(1e-20)                       # scale below 2^-64: IEEE division path
+    x[11] *= np.exp2(np.arange(cols) % 61 - 30).astype(np.float32)  # wide exponent range per block
     xb = orc.f32_to_bf16(x)
     xf = orc.bf16_to_f32(xb)
     q_ref, s_ref = orc.quant_rows_1x128(xf)
