@@ -457,24 +457,22 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? 0.0f : -FLT_MAX;
-    // the partials of 8 chunks are loaded before any is added, then summed
-    // in chunk order
-    for (int s0 = 0; s0 < nsplit; s0 += 8) {
-        float pv[8][4];
+    // every chunk's partials (nsplit <= kRtMaxSplit) are loaded before any
+    // is added -- one round trip -- then summed in chunk order
+    static_assert(kRtMaxSplit == 16, "one batch of 16 chunk loads");
+    float pv[kRtMaxSplit][4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float* row = part + ((size_t)(s0 + i) * T + t) * E;
+    for (int i = 0; i < kRtMaxSplit; i++) {
+        const float* row = part + ((size_t)i * T + t) * E;
+#pragma unroll
+        for (int j = 0; j < 4; j++) pv[i][j] = i < nsplit && lane + 64 * j < E ? row[lane + 64 * j] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kRtMaxSplit; i++)
+        if (i < nsplit)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                pv[i][j] = s0 + i < nsplit && lane + 64 * j < E ? row[lane + 64 * j] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (s0 + i < nsplit)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (lane + 64 * j < E) v[j] = add_rn(v[j], pv[i][j]);
-    }
+                if (lane + 64 * j < E) v[j] = add_rn(v[j], pv[i][j]);
     wave_route_token_reg<KMAX>(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
@@ -516,6 +514,7 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
     const bool quant = xq != nullptr;
     AMDMOE_CHECK_ARG(!quant || (xs && D % 128 == 0), "routing: fused quantisation needs D %% 128 == 0");
     const RouteSplit sp = route_split(T, D, quant);
+    AMDMOE_CHECK_ARG(sp.nsplit >= 1 && sp.nsplit <= kRtMaxSplit, "routing: %d gate splits", sp.nsplit);
     static bool attr_set = false;
     if (!attr_set) {
         AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)route_logits_kernel,
