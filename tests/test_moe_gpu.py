@@ -423,6 +423,16 @@ def test_forward_fp8_small_full(amd, orc):
     assert _fp8_case(amd, orc, w, 64, 16, 4, 512, 256) < 2e-2
 
 
+@pytest.mark.parametrize("T", [2, 16, 17])
+def test_forward_fp8_decode_sizes(amd, orc, T):
+    """Decode-sized batches: a few tokens over many experts (most M-tiles
+    one 16-row token tile), parity with the oracle's fp8 forward."""
+    import synth
+    announce(f"forward_fp8 decode size T={T}")
+    w = synth.dsv3_weights(16, 512, 256, seed=78)
+    assert _fp8_case(amd, orc, w, T, 16, 4, 512, 256) < 2e-2
+
+
 def test_forward_fp8_multi_mtile_experts(amd, orc):
     """~256 rows per expert (as DeepSeek-V3 at T=8192): experts take one or
     two M-tiles."""
