@@ -178,6 +178,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // `size` bytes at M0 + l*size, where M0 is the (wave-uniform) LDS pointer.
 // A voffset past the descriptor's range reads as zeros.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gptr_t;  // a global-memory pointer (global_load_lds)
 constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
 constexpr uint32_t kOob = 0x80000000u;   // voffset that fails the range check
 

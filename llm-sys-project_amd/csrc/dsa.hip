@@ -727,7 +727,18 @@ __device__ __forceinline__ void s_mfma4(f32x4 (&c)[2][2], const u32x4& a0, const
             : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
 }
 
-__global__ __launch_bounds__(256, 1) void dsa_split_kernel(
+// 1152 zero bytes: the latent row an invalid position reads when the cache
+// is addressed with 64-bit pointers (caches beyond the 4 GiB that a buffer
+// descriptor's 32-bit offsets reach)
+static __device__ __align__(16) uint16_t g_dsa_zero_row[kDt];
+
+// WIDE: the cache is addressed with 64-bit per-lane pointers
+// (global_load_lds_dwordx4) instead of a buffer descriptor's 32-bit offsets.
+// The body is a device template behind two plain kernels (the host side
+// dropped the launch stub of a templated kernel instantiation using buffer
+// descriptors).
+template <bool WIDE>
+__device__ __forceinline__ void dsa_split_body(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
     const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
     const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,
@@ -812,20 +823,37 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     // wave w issues blocks w, w + 4, ..., w + 32.  The chunk-group offset goes
     // in soffset (an instruction immediate would also move the LDS address).
     const uint32_t lane_c16 = 16u * (uint32_t)((lane & 3) ^ hsw((lane >> 4) & 3));
-    auto row_vo = [&](int tok) __attribute__((always_inline)) {
-        uint32_t vo = kOobDsa;
-        if (tok < len) {
-            const long r = s_rows[tok];
-            const long off = r * kRowBytes + lane_c16;
-            if (r >= 0 && off < cache_bytes) vo = (uint32_t)off;
+    // a token's row: its 32-bit offset (an out-of-range one reads zeros) or,
+    // WIDE, its address (the zero row for an invalid position)
+    using RowAddr = std::conditional_t<WIDE, const uint8_t*, uint32_t>;
+    auto row_vo = [&](int tok) __attribute__((always_inline)) -> RowAddr {
+        if constexpr (WIDE) {
+            const uint8_t* a = (const uint8_t*)g_dsa_zero_row + lane_c16;
+            if (tok < len) {
+                const long r = s_rows[tok];
+                const long off = r * kRowBytes + lane_c16;
+                if (r >= 0 && off < cache_bytes) a = (const uint8_t*)cache + off;
+            }
+            return a;
+        } else {
+            uint32_t vo = kOobDsa;
+            if (tok < len) {
+                const long r = s_rows[tok];
+                const long off = r * kRowBytes + lane_c16;
+                if (r >= 0 && off < cache_bytes) vo = (uint32_t)off;
+            }
+            return vo;
         }
-        return vo;
     };
-    auto issue_blk = [&](int st, uint32_t vo0, uint32_t vo1, int n) __attribute__((always_inline)) {
+    auto issue_blk = [&](int st, RowAddr vo0, RowAddr vo1, int n) __attribute__((always_inline)) {
         const int b = wave + 4 * n;
         const int tg = b >= 18 ? 1 : 0;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rc, (lds_ptr_t)(smem + st * kStage32 + b * 1024), 16, tg ? vo1 : vo0, 64 * (b - 18 * tg), 0, 0);
+        if constexpr (WIDE)
+            __builtin_amdgcn_global_load_lds((gptr_t)((tg ? vo1 : vo0) + 64 * (b - 18 * tg)),
+                                             (lds_ptr_t)(smem + st * kStage32 + b * 1024), 16, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rc, (lds_ptr_t)(smem + st * kStage32 + b * 1024), 16, tg ? vo1 : vo0, 64 * (b - 18 * tg), 0, 0);
     };
 
     f32x4 o[32][2];  // dims 16mt + 4g + i, head hbase + 16ht + c16
@@ -877,13 +905,13 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     // so every iteration waits for the same count)
 #pragma unroll
     for (int i = 0; i < kRing32 - 1; i++) {
-        const uint32_t a = row_vo(kT32 * i + (lane >> 2)), b = row_vo(kT32 * i + 16 + (lane >> 2));
+        const RowAddr a = row_vo(kT32 * i + (lane >> 2)), b = row_vo(kT32 * i + 16 + (lane >> 2));
 #pragma unroll
         for (int n = 0; n < 9; n++) issue_blk(i, a, b, n);
     }
     for (int t = 0; t < ntiles; t++) {
         const int tn = t + kRing32 - 1;
-        const uint32_t nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
+        const RowAddr nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
         wait_vmcnt<9 * (kRing32 - 2)>();  // tile t landed (this wave's part)
         bare_barrier();                   // ... everywhere; stage tn % 4 is free
         uint32_t soff = (t % kRing32) * kStage32;
@@ -1025,6 +1053,20 @@ __global__ __launch_bounds__(256, 1) void dsa_split_kernel(
     }
 }
 
+#define AMDMOE_DSA_SPLIT_KERNEL(NAME, W)                                                              \
+    __global__ __launch_bounds__(256, 1) void NAME(                                                   \
+        const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,                             \
+        const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,     \
+        const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,     \
+        uint16_t* __restrict__ part_b, float* __restrict__ part_ml, int Q, int H, int S, int page,    \
+        int pages_per_seq, int nsplit, int chunk, float scale_log2) {                                 \
+        dsa_split_body<W>(qn, qp, cache, cache_bytes, page_table, logical, part_o, spare_o, part_b,   \
+                          part_ml, Q, H, S, page, pages_per_seq, nsplit, chunk, scale_log2);          \
+    }
+AMDMOE_DSA_SPLIT_KERNEL(dsa_split_kernel, false)
+AMDMOE_DSA_SPLIT_KERNEL(dsa_split_wide_kernel, true)
+#undef AMDMOE_DSA_SPLIT_KERNEL
+
 // Combines the splits of dsa_split_kernel: per (query, head), m = max of
 // the split maxima, weights c_j = 2^(m_j - m), out = (sum c_j O_j) /
 // (sum c_j l_j), bf16.  Workgroup = one query x 16 heads (one partial block),
@@ -1101,8 +1143,12 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
     AMDMOE_CHECK_ARG(H % 32 == 0 && H > 0, "dsa_decode_bf16_paged: H=%d not a multiple of 32", H);
     AMDMOE_CHECK_ARG(S >= 1 && S <= kMaxS, "dsa_decode_bf16_paged: S=%d outside [1, %d]", S, kMaxS);
     AMDMOE_CHECK_ARG(page >= 1 && pages_per_seq >= 1, "dsa_decode_bf16_paged: bad paging");
-    AMDMOE_CHECK_ARG(cache_tokens >= 1 && cache_tokens * kRowBytes <= kMaxCacheBytes,
-                     "dsa_decode_bf16_paged: cache of %ld tokens outside (0, 4 GiB)", cache_tokens);
+    // caches beyond 4 GiB: the split kernel addresses them with 64-bit
+    // pointers; the kernels for H not a multiple of 128 use 32-bit offsets
+    AMDMOE_CHECK_ARG(cache_tokens >= 1 && (cache_tokens * kRowBytes <= kMaxCacheBytes || H % 128 == 0),
+                     "dsa_decode_bf16_paged: cache of %ld tokens outside (0, 4 GiB) (larger caches need H a "
+                     "multiple of 128)", cache_tokens);
+    const bool wide = cache_tokens * kRowBytes > kMaxCacheBytes;
     if (Q == 0) return AMDMOE_OK;
     const float scale_log2 = 1.0f / sqrtf((float)(Dc + Dp)) * 1.4426950408889634f;
     if (H % 128 == 0) {
@@ -1113,18 +1159,15 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                          "dsa_decode_bf16_paged: scratch of %zu bytes, %zu needed", scratch_bytes, need);
         const long grid = ceil_div((long)Q * (H / 128) * ns, 8) * 8;
         AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_decode_bf16_paged: grid too large");
-        static bool attr_split = false;
-        if (!attr_split) {
-            AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_split_kernel,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDsaSplitLds));
-            attr_split = true;
-        }
         const size_t rows_bytes = (size_t)Q * ns * H * kDc * 4;
         float* part_o = (float*)scratch;
         float* spare_o = (float*)((uint8_t*)scratch + rows_bytes);
         uint16_t* part_b = (uint16_t*)((uint8_t*)scratch + 2 * rows_bytes);
         float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes + rows_bytes / 2);
-        hipLaunchKernelGGL(dsa_split_kernel, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
+        auto split = wide ? dsa_split_wide_kernel : dsa_split_kernel;
+        const int rc = ensure_dynamic_lds((const void*)split, kDsaSplitLds);
+        if (rc != AMDMOE_OK) return rc;
+        hipLaunchKernelGGL(split, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
                            qp, cache, cache_tokens * kRowBytes, page_table, logical, part_o, spare_o,
                            part_b, part_ml, Q, H, S, page, pages_per_seq, ns, chunk, scale_log2);
         AMDMOE_LAUNCH_CHECK();
@@ -1137,23 +1180,17 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
     const int nblk = Q * (H / 32);
     const int grid = (nblk + 7) / 8 * 8;  // padded for the XCD remap; padding blocks exit
     if (S <= kMaxS64) {
-        static bool attr64_set = false;
-        if (!attr64_set) {
-            AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_bf16_paged64_kernel,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDsa64Lds));
-            attr64_set = true;
-        }
+        const int rc = ensure_dynamic_lds((const void*)dsa_bf16_paged64_kernel, kDsa64Lds);
+        if (rc != AMDMOE_OK) return rc;
         hipLaunchKernelGGL(dsa_bf16_paged64_kernel, dim3(grid), dim3(256), kDsa64Lds, st, qn, qp,
                            cache, cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,
                            pages_per_seq, scale_log2);
         AMDMOE_LAUNCH_CHECK();
         return AMDMOE_OK;
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)dsa_bf16_paged_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kDsaLds));
-        attr_set = true;
+    {
+        const int rc = ensure_dynamic_lds((const void*)dsa_bf16_paged_kernel, kDsaLds);
+        if (rc != AMDMOE_OK) return rc;
     }
     hipLaunchKernelGGL(dsa_bf16_paged_kernel, dim3(grid), dim3(256), kDsaLds, st, qn, qp, cache,
                        cache_tokens * kRowBytes, page_table, logical, out, Q, H, S, page,

@@ -2,9 +2,28 @@
 // and the grouped-GEMM argument block).  Not part of the public ABI.
 #pragma once
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "common.hpp"
 
 namespace amdmoe {
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per (kernel, device) -- the attribute is per device -- under a lock, so
+// concurrent first launches from several threads are safe.
+inline int ensure_dynamic_lds(const void* fn, int bytes) {
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = -1;
+    AMDMOE_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({fn, dev})) return AMDMOE_OK;
+    AMDMOE_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    done.insert({fn, dev});
+    return AMDMOE_OK;
+}
 
 enum { DT_F32 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_MX = 3 };  // DT_MX: MXFP4 weights x MXFP8 activations
 enum { MODE_UP = 0, MODE_DOWN = 1 };

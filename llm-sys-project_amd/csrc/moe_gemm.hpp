@@ -911,11 +911,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
 // ---------------------------------------------------------------- launch
 template <int DT, int MODE, bool PK>
 int launch_gemm_variant(const GemmArgs& g, long max_tiles, hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)grouped_gemm_kernel<DT, MODE, PK>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds));
-        attr_set = true;
+    {
+        const int rc = ensure_dynamic_lds((const void*)grouped_gemm_kernel<DT, MODE, PK>, kGemmLds);
+        if (rc != AMDMOE_OK) return rc;
     }
     long work = max_tiles * g.n_tiles_n;
     long grid = 8 * ceil_div(work, 8);

@@ -515,11 +515,9 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
     AMDMOE_CHECK_ARG(!quant || (xs && D % 128 == 0), "routing: fused quantisation needs D %% 128 == 0");
     const RouteSplit sp = route_split(T, D, quant);
     AMDMOE_CHECK_ARG(sp.nsplit >= 1 && sp.nsplit <= kRtMaxSplit, "routing: %d gate splits", sp.nsplit);
-    static bool attr_set = false;
-    if (!attr_set) {
-        AMDMOE_HIP_TRY(hipFuncSetAttribute((const void*)route_logits_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kRtLds));
-        attr_set = true;
+    {
+        const int rc = ensure_dynamic_lds((const void*)route_logits_kernel, kRtLds);
+        if (rc != AMDMOE_OK) return rc;
     }
     // one linear grid, padded to a multiple of 8 for the XCD dealing
     const long items = ceil_div(T, kRtTok) * (long)sp.nsplit;

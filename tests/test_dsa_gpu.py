@@ -266,3 +266,43 @@ def test_dsa_f32_beyond_lds_s20000(amd, orc):
     err = np.abs(out.cpu().numpy() - ref).max()
     print(f"S=20000: max_err={err:.3e}")
     assert err < 1e-6
+
+
+def test_dsa_bf16_paged_cache_beyond_4gib(amd, orc):
+    """A latent cache of 4.6 GB (beyond the 32-bit offsets of a buffer
+    descriptor): half of each query's pages lie above 4 GiB.  The split
+    kernel's 64-bit-address variant matches the oracle, and is bit-identical
+    to the 32-bit-offset kernel on a compacted copy of the same pages."""
+    Q, H, S, page, pps = 2, 128, 512, 64, 64
+    N = 4_000_000                                    # cache tokens (4.6 GB)
+    print(f"dsa_bf16 cache of {N} tokens ({N * 1152 / 2**30:.2f} GiB)", flush=True)
+    rng = np.random.default_rng(4)
+    n_pages = N // page
+    hi0 = (1 << 32) // (page * 1152) + 1             # first page wholly above 4 GiB
+    pages = np.concatenate([rng.choice(hi0, Q * pps // 2, replace=False),
+                            rng.choice(np.arange(hi0, n_pages), Q * pps // 2, replace=False)])
+    rng.shuffle(pages)
+    pt = pages.reshape(Q, pps).astype(np.int32)
+    cache = torch.empty((N, 576), dtype=torch.int16, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    rows = torch.from_numpy((pages[:, None] * page + np.arange(page)[None, :]).reshape(-1)).cuda()
+    vals = torch.randn((rows.numel(), 576), generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    cache.index_copy_(0, rows, vals)
+    logical = np.stack([rng.permutation(pps * page)[:S] for _ in range(Q)]).astype(np.int32)
+    qn = torch.randn((Q, H, 512), generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    qp = torch.randn((Q, H, 64), generator=g, device="cuda").to(torch.bfloat16).view(torch.int16)
+    inputs = (qn, qp, cache, dev(pt), dev(logical), pps)
+    err = _paged_case(amd, orc, Q, H, S, N // Q, page=page, inputs=inputs)
+    assert err < 2e-2
+    # the same pages compacted into a cache below 4 GiB: the 32-bit kernel
+    out_w = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
+    amd.dsa_decode_bf16_paged(qn, qp, cache, dev(pt), dev(logical), out_w,
+                              amd.dsa_config(Q, H, 512, 64, S, page, N), pps)
+    small = cache.index_select(0, rows).contiguous()
+    del cache
+    pt_small = np.arange(Q * pps, dtype=np.int32).reshape(Q, pps)
+    out_s = torch.empty_like(out_w)
+    amd.dsa_decode_bf16_paged(qn, qp, small, dev(pt_small), dev(logical), out_s,
+                              amd.dsa_config(Q, H, 512, 64, S, page, small.shape[0]), pps)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out_w.cpu().numpy(), out_s.cpu().numpy())
