@@ -316,8 +316,9 @@ int amdmoe_dsa_forward_f32(const float* q_nope, const float* q_pe, const float* 
  * output is attention over the valid positions only (0 for a query with
  * none).  The -1 padding of amdmoe_dsa_indexer_topk_fp8 (sequences shorter
  * than the selection) is therefore decoded correctly.
- * Requires Dc == 512, Dp == 64, H a multiple of 32, 1 <= S <= 4096; a cache
- * of more than 4 GiB (about 3.7 M tokens) needs H a multiple of 128. */
+ * Requires Dc == 512, Dp == 64, H a multiple of 32, 1 <= S <= 4096; for H a
+ * multiple of 128, S up to 65536 and caches of more than 4 GiB (about 3.7 M
+ * tokens) are accepted. */
 int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
                                  const uint16_t* cache, const int* page_table,
                                  const int* logical_indices, uint16_t* output,

@@ -680,6 +680,7 @@ constexpr int kT32 = 32;
 constexpr int kStage32 = kT32 * kRowBytes;                // 36864
 constexpr int kRing32 = 4;
 constexpr int kMaxChunk = 2048;                           // tokens per split
+constexpr int kMaxSplitS = 65536;                         // selected positions per query (32 splits)
 constexpr int kRows32Off = kRing32 * kStage32;            // 147456
 constexpr int kMask32Off = kRows32Off + kMaxChunk * 4;    // 155648: validity bits, 64 tokens per word
 constexpr int kDsaSplitLds = kMask32Off + kMaxChunk / 8;  // 155904
@@ -1141,7 +1142,11 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                           int pages_per_seq, void* scratch, size_t scratch_bytes, hipStream_t st) {
     AMDMOE_CHECK_ARG(Dc == kDc && Dp == kDp, "dsa_decode_bf16_paged: needs Dc=512, Dp=64 (got %d, %d)", Dc, Dp);
     AMDMOE_CHECK_ARG(H % 32 == 0 && H > 0, "dsa_decode_bf16_paged: H=%d not a multiple of 32", H);
-    AMDMOE_CHECK_ARG(S >= 1 && S <= kMaxS, "dsa_decode_bf16_paged: S=%d outside [1, %d]", S, kMaxS);
+    // the split kernel (H a multiple of 128) takes any S up to kMaxSplitS in
+    // more splits; the others hold a query's rows in LDS
+    AMDMOE_CHECK_ARG(S >= 1 && S <= (H % 128 == 0 ? kMaxSplitS : kMaxS),
+                     "dsa_decode_bf16_paged: S=%d outside [1, %d] for H=%d", S,
+                     H % 128 == 0 ? kMaxSplitS : kMaxS, H);
     AMDMOE_CHECK_ARG(page >= 1 && pages_per_seq >= 1, "dsa_decode_bf16_paged: bad paging");
     // caches beyond 4 GiB: the split kernel addresses them with 64-bit
     // pointers; the kernels for H not a multiple of 128 use 32-bit offsets

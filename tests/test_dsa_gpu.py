@@ -306,3 +306,10 @@ def test_dsa_bf16_paged_cache_beyond_4gib(amd, orc):
                               amd.dsa_config(Q, H, 512, 64, S, page, small.shape[0]), pps)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out_w.cpu().numpy(), out_s.cpu().numpy())
+
+
+def test_dsa_bf16_paged_long_selection(amd, orc):
+    """H = 128 with 10000 selected positions per query (beyond the 4096 that
+    the one-workgroup-per-query kernels hold): more splits, same result."""
+    print("dsa_bf16 S=10000", flush=True)
+    assert _paged_case(amd, orc, 2, 128, 10000, 16384) < 2e-2
