@@ -80,7 +80,7 @@ constexpr int kRowInfoOff = kBScaleOff + 2 * kMaxKb * 4;  // DOWN: [256] slot, [
 constexpr int kGemmLds = kRowInfoOff + kBM * 8;           // 107520
 static_assert(kEpiRows * kEpiPitch * 4 <= kNS * kStageBytes, "epilogue staging fits the ring");
 static_assert(kBM == 256, "the wave layout assumes 256-row tiles");
-static_assert(128 * 544 <= kNS * kStageBytes, "DOWN epilogue staging fits the ring");
+static_assert(128 * 528 <= kNS * kStageBytes, "DOWN epilogue staging fits the ring");
 
 template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
@@ -870,11 +870,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
         } else {
             // bf16: the weighted rows are staged through the (now idle) ring,
-            // 128 rows per pass as bf16 with a 544-byte pitch (16 rows of a
-            // 32-byte piece hit each bank at most twice), then every thread
-            // stores 16 contiguous bytes: one instruction writes two full
-            // 512-byte row segments instead of 16 rows x 32 bytes
-            constexpr int kPitch = 544;
+            // 128 rows per pass as bf16 with a 528-byte pitch (132 dwords, 4
+            // mod 64: the 16 rows x 8 bytes of a half-wave's write land on 64
+            // distinct banks -- a 544-byte pitch put rows r and r + 8 on the
+            // same banks), then every thread stores 16 contiguous bytes: one
+            // instruction writes two full 512-byte row segments instead of 16
+            // rows x 32 bytes
+            constexpr int kPitch = 528;
             uint8_t* stg = smem;
 #pragma unroll
             for (int half = 0; half < 2; half++) {
