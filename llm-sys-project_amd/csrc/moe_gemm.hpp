@@ -870,14 +870,19 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
         } else {
             // bf16: the weighted rows are staged through the (now idle) ring,
-            // 128 rows per pass as bf16 with a 528-byte pitch (132 dwords, 4
-            // mod 64: the 16 rows x 8 bytes of a half-wave's write land on 64
-            // distinct banks -- a 544-byte pitch put rows r and r + 8 on the
-            // same banks), then every thread stores 16 contiguous bytes: one
-            // instruction writes two full 512-byte row segments instead of 16
-            // rows x 32 bytes
+            // 128 rows per pass as bf16, then every thread stores 16
+            // contiguous bytes: one instruction writes two full 512-byte row
+            // segments instead of 16 rows x 32 bytes.
+            // Staging write: lane (q, r16) holds columns 4q..4q+3 of both
+            // column tiles.  v_permlane16_swap exchanges lane group q = 1's
+            // ct = 0 half with group q = 0's ct = 1 half (and likewise 3 / 2),
+            // so each lane then holds 8 consecutive columns, 16 * (q & 1) +
+            // 8 * (q >> 1) onwards, of one tile, and writes them as one 16-byte
+            // piece.  With a 528-byte pitch (132 dwords, 4 mod 64) the 16 rows
+            // of a lane group land on 16 distinct 4-bank groups.
             constexpr int kPitch = 528;
             uint8_t* stg = smem;
+            const int col = 32 * wave + 16 * (q & 1) + 8 * (q >> 1);
 #pragma unroll
             for (int half = 0; half < 2; half++) {
                 if (128 * half >= rows) continue;  // uniform
@@ -886,12 +891,12 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 for (int r8 = 0; r8 < 8; r8++) {
                     const int rt = 8 * half + r8;
                     const float wgt = s_wt[16 * rt + r16];
-#pragma unroll
-                    for (int ct = 0; ct < 2; ct++) {
-                        const f32x4 v = acc[rt][ct] * wgt;
-                        *(u32x2*)(stg + (16 * r8 + r16) * kPitch + (32 * wave + 16 * ct + 4 * q) * 2) =
-                            (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                    }
+                    const f32x4 v0 = acc[rt][0] * wgt, v1 = acc[rt][1] * wgt;
+                    const auto s0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v0[0], v0[1]),
+                                                                     pack_bf16x2(v1[0], v1[1]), false, false);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v0[2], v0[3]),
+                                                                     pack_bf16x2(v1[2], v1[3]), false, false);
+                    *(u32x4*)(stg + (16 * r8 + r16) * kPitch + col * 2) = (u32x4){s0[0], s1[0], s0[1], s1[1]};
                 }
                 lds_barrier();
     #pragma unroll
