@@ -770,11 +770,15 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             const int col = nt * 128 + 32 * pp;
             const bool ok = rr < rows && col < g.n_out;
             // eight unconditional 16-byte reads (the staged row is in LDS
-            // whether or not it is stored), zeroed where not stored
+            // whether or not it is stored), zeroed where not stored.  Parts
+            // pp and pp + 2 of a row lie 128 bytes apart, on the same banks,
+            // so parts 2 and 3 read their columns rotated by 16: v[s] holds
+            // column (s + 16 rot) mod 32, and the stores below undo it
+            const int rot = pp >> 1;
             float v[32];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const f32x4 t = *(const f32x4*)&Tb[er * kEpiPitch + 32 * pp + 4 * j];
+                const f32x4 t = *(const f32x4*)&Tb[er * kEpiPitch + 32 * pp + 4 * ((j + 4 * rot) & 7)];
                 for (int i = 0; i < 4; i++) v[4 * j + i] = ok ? t[i] : 0.0f;
             }
             const size_t pos = (size_t)row0 + rr;
@@ -802,8 +806,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                                                         v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
                     }
                     uint8_t* dst = g.out + pos * g.n_out + col;
-                    *(u32x4*)dst = o0;
-                    *(u32x4*)(dst + 16) = o1;
+                    *(u32x4*)(dst + 16 * rot) = o0;
+                    *(u32x4*)(dst + 16 - 16 * rot) = o1;
                     if (pp == 0) g.out_scale[(size_t)nt * g.out_scale_rows + pos] = s;
                 }
             } else if (DT == DT_MX) {
@@ -824,8 +828,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                                                 v[16 + 4 * k + 2] * inv, v[16 + 4 * k + 3] * inv);
                     }
                     uint8_t* dst = g.out + pos * g.n_out + col;
-                    *(u32x4*)dst = o0;
-                    *(u32x4*)(dst + 16) = o1;
+                    *(u32x4*)(dst + 16 * rot) = o0;
+                    *(u32x4*)(dst + 16 - 16 * rot) = o1;
                     ((uint8_t*)g.out_scale)[((size_t)(col / 128) * g.out_scale_rows + pos) * 4 + (col / 32) % 4] =
                         (uint8_t)e8;
                 }
@@ -835,14 +839,15 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     for (int k = 0; k < 4; k++) {
                         u32x4 o;
                         for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(v[8 * k + 2 * m], v[8 * k + 2 * m + 1]);
-                        *(u32x4*)(dst + 16 * k) = o;
+                        *(u32x4*)(dst + 16 * ((k + 2 * rot) & 3)) = o;
                     }
                 }
             } else {
                 if (ok) {
                     float* dst = (float*)g.out + pos * g.n_out + col;
                     for (int k = 0; k < 8; k++)
-                        *(f32x4*)(dst + 4 * k) = (f32x4){v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+                        *(f32x4*)(dst + 4 * ((k + 4 * rot) & 7)) =
+                            (f32x4){v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
                 }
             }
         }
