@@ -643,39 +643,40 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
 
 // ------------------------------------------------------ split kernel
 // dsa_split_kernel (H a multiple of 128): one workgroup per (query, group
-// of 128 heads, token split), 4 waves; wave w owns heads 32w..32w+31 of the
+// of 128 heads, token split), 8 waves; wave w owns heads 16w..16w+15 of the
 // group for all of the split's tokens, so its softmax state is private (no
 // exchange between waves) and P goes from the S^T accumulators straight
 // into the PV MFMA operand.  32-token tiles stream through a 4-stage LDS
 // ring (three tiles in flight), filled by direct global->LDS loads; each
 // wave reads every tile once for S and once for V.
-//   S^T (16 tokens x 16 heads) = K . Q^T   16x16x32 bf16, 2 token x 2 head
-//                                          tiles, q of 32 heads in registers
+//   S^T (16 tokens x 16 heads) = K . Q^T   16x16x32 bf16, 2 token tiles,
+//                                          q of the wave's 16 heads in
+//                                          registers
 //   online softmax per head in the exp2 domain; l is kept per lane and
 //     reduced once at the end
 //   O^T (512 dims x 16 heads) += V^T . P^T  16x16x32 bf16 in the token
 //     order of S^T's output layout: lane (head c, group g) holds tokens
 //     4g..4g+3 and 16+4g..16+4g+3, and the transposed LDS reads of V^T
 //     fetch the same tokens
-// Registers: O is 256 accumulators (the whole AGPR file) and q 144 VGPRs,
-// so (1) the S^T MFMAs write VGPRs, and (2) O is never read or written by
-// the VALU (which would make the compiler shuttle all of it between register
-// files): O leaves the AGPRs only through stores.  The running max m is
-// raised only when a tile max exceeds it by more than 8 (so p <= 256); then
-// the wave stores O to its spare rows B, adds B into its partial rows A in
-// memory, scaled to the new max, and restarts O at zero.  This is a rare
-// path: with O(1) scores the first tile's max is never exceeded by 8.
+// Registers: O is 128 accumulators and q 72, so a wave fits in 256
+// registers and two waves share each SIMD (one wave's softmax, LDS waits
+// and barrier run under the other's MFMAs).  The price is LDS traffic:
+// every wave reads each tile for its 16 heads, 544 KB per CU per tile.  The
+// running max m is raised only when a tile max exceeds it by more than 8
+// (so p <= 256), and then O and l are multiplied by 2^(m_old - m_new) in
+// registers; with O(1) scores the first tile's max is never exceeded by 8.
 // Every split writes its unnormalised O (bf16: the output is bf16 and the
 // merge sums at most a few splits in fp32) and (max, sum) per head;
-// dsa_merge_kernel combines the splits and writes bf16.  The fp32 rows A and
-// B serve only the rare rescale path.
+// dsa_merge_kernel combines the splits and writes bf16.
 //
 // Tile layout (tile32_off): 1 KB blocks of 16 tokens x 4 chunks (16-byte
 // chunk j of the 1152-byte row), blocks [token group][chunk group], within a
-// block [token][slot] with slot = (j & 3) ^ hsw(token bits 2-3).  hsw swaps
-// the two bits, which keeps the 16-token fragment reads of S conflict-free
-// and puts the two 4-token groups of a transposed V read in different halves
-// of each 64-byte window.
+// block [token][slot] with slot = (j & 3) ^ (token bits 1-2).  Measured with
+// the bank-conflict counter on gfx950, this is free of conflicts for both the
+// 16-token S fragment reads (ds_read_b128, lane = token, one chunk) and the
+// transposed V^T reads (ds_read_b64_tr_b16, 4 tokens x 2 chunks per 16
+// lanes); XOR-ing token bits 2-3 instead (the plain 64-bank model's answer)
+// cost the S reads 4 conflict cycles each.
 constexpr int kT32 = 32;
 constexpr int kStage32 = kT32 * kRowBytes;                // 36864
 constexpr int kRing32 = 4;
@@ -685,47 +686,8 @@ constexpr int kRows32Off = kRing32 * kStage32;            // 147456
 constexpr int kMask32Off = kRows32Off + kMaxChunk * 4;    // 155648: validity bits, 64 tokens per word
 constexpr int kDsaSplitLds = kMask32Off + kMaxChunk / 8;  // 155904
 
-__device__ __forceinline__ int hsw(int a) { return ((a & 1) << 1) | (a >> 1); }
 __device__ __forceinline__ int tile32_off(int t, int j) {  // token t (0..31), chunk j (0..71)
-    return ((t >> 4) * 18 + (j >> 2)) * 1024 + (t & 15) * 64 + (((j & 3) ^ hsw((t >> 2) & 3)) << 4);
-}
-
-// Four VGPR-form MFMAs of one S^T K-step (token tiles x head tiles), as asm
-// with the wait states the compiler would add for them: 2 after a VALU
-// write of an operand (leading s_nop 1); FIRST: accumulators start at 0;
-// LAST: 16 wait states before any other instruction reads the results.
-template <bool FIRST, bool LAST>
-__device__ __forceinline__ void s_mfma4(f32x4 (&c)[2][2], const u32x4& a0, const u32x4& a1,
-                                        const u32x4& q0, const u32x4& q1) {
-    if (FIRST)
-        asm volatile(
-            "s_nop 1\n\t"
-            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, 0\n\t"
-            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, 0\n\t"
-            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, 0\n\t"
-            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, 0"
-            : "=&v"(c[0][0]), "=&v"(c[0][1]), "=&v"(c[1][0]), "=&v"(c[1][1])
-            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
-    else if (!LAST)
-        asm volatile(
-            "s_nop 1\n\t"
-            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, %0\n\t"
-            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, %1\n\t"
-            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, %2\n\t"
-            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, %3"
-            : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])
-            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
-    else
-        asm volatile(
-            "s_nop 1\n\t"
-            "v_mfma_f32_16x16x32_bf16 %0, %4, %6, %0\n\t"
-            "v_mfma_f32_16x16x32_bf16 %1, %4, %7, %1\n\t"
-            "v_mfma_f32_16x16x32_bf16 %2, %5, %6, %2\n\t"
-            "v_mfma_f32_16x16x32_bf16 %3, %5, %7, %3\n\t"
-            "s_nop 7\n\t"
-            "s_nop 7"
-            : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[1][0]), "+v"(c[1][1])
-            : "v"(a0), "v"(a1), "v"(q0), "v"(q1));
+    return ((t >> 4) * 18 + (j >> 2)) * 1024 + (t & 15) * 64 + (((j & 3) ^ ((t >> 1) & 3)) << 4);
 }
 
 // 1152 zero bytes: the latent row an invalid position reads when the cache
@@ -738,13 +700,14 @@ static __device__ __align__(16) uint16_t g_dsa_zero_row[kDt];
 // The body is a device template behind two plain kernels (the host side
 // dropped the launch stub of a templated kernel instantiation using buffer
 // descriptors).
+constexpr int kRowsPer8 = kMaxChunk / 512;  // split positions per thread
+
 template <bool WIDE>
 __device__ __forceinline__ void dsa_split_body(
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,
     const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,
-    const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,
-    uint16_t* __restrict__ part_b, float* __restrict__ part_ml, int Q, int H,
-    int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
+    const int* __restrict__ logical, uint16_t* __restrict__ part_b, float* __restrict__ part_ml, int Q,
+    int H, int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     int* s_rows = (int*)(smem + kRows32Off);
     unsigned long long* s_mask = (unsigned long long*)(smem + kMask32Off);
@@ -764,68 +727,64 @@ __device__ __forceinline__ void dsa_split_body(
     const int t0 = sp * chunk;
     const int len = max(0, min(S, t0 + chunk) - t0);
     const int g = lane >> 4, c16 = lane & 15;
-    const int hbase = 128 * hg + 32 * wave;  // this wave's first head
+    const int hbase = 128 * hg + 16 * wave;  // this wave's first head
 
     // Prologue, ordered so the q loads overlap the two dependent loads of
     // the page-table translation: logical indices, then page-table entries,
-    // then q (36 loads per lane), then wait for all but the q loads.  The
+    // then q (18 loads per lane), then wait for all but the q loads.  The
     // q loads are waited for (by the compiler) at tile 0's first S step.
     // A token is valid when its logical index lies in [0, pages_per_seq *
     // page), its page id is >= 0 and its row inside the cache; an invalid
     // one (e.g. the -1 padding of a sequence shorter than the selection)
     // reads no page-table entry, loads a zero row and scores -inf.
-    constexpr int kRowsPer = kMaxChunk / 256;
-    int li[kRowsPer], pg[kRowsPer];
+    int li[kRowsPer8], pg[kRowsPer8];
     {
         const int* lg = logical + (size_t)qi * S + t0;
         const int* pt = page_table + (size_t)qi * pages_per_seq;
         const long seq = (long)pages_per_seq * page;
 #pragma unroll
-        for (int k = 0; k < kRowsPer; k++) li[k] = tid + 256 * k < len ? lg[tid + 256 * k] : -1;
+        for (int k = 0; k < kRowsPer8; k++) li[k] = tid + 512 * k < len ? lg[tid + 512 * k] : -1;
 #pragma unroll
-        for (int k = 0; k < kRowsPer; k++) {
+        for (int k = 0; k < kRowsPer8; k++) {
             const bool ok = li[k] >= 0 && li[k] < seq;
             if (!ok) li[k] = -1;
             pg[k] = ok ? pt[li[k] / page] : -1;
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // q of heads hbase + 16ht + c16 as B fragments: K-step ks = 32 dims, group g holds 8
-    u32x4 qf[2][18];
-#pragma unroll
-    for (int ht = 0; ht < 2; ht++) {
-        const size_t hrow = (size_t)qi * H + hbase + 16 * ht + c16;
+    // q of head hbase + c16 as B fragments: K-step ks = 32 dims, group g holds 8
+    u32x4 qf[18];
+    {
+        const size_t hrow = (size_t)qi * H + hbase + c16;
         const uint16_t* qnr = qn + hrow * kDc;
         const uint16_t* qpr = qp + hrow * kDp;
 #pragma unroll
-        for (int ks = 0; ks < 16; ks++) qf[ht][ks] = *(const u32x4*)(qnr + 32 * ks + 8 * g);
+        for (int ks = 0; ks < 16; ks++) qf[ks] = *(const u32x4*)(qnr + 32 * ks + 8 * g);
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) qf[ht][16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
+        for (int ks = 0; ks < 2; ks++) qf[16 + ks] = *(const u32x4*)(qpr + 32 * ks + 8 * g);
     }
     __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<36>();  // every page-table entry has arrived
+    wait_vmcnt<18>();  // every page-table entry has arrived
     {
         const long cache_rows = cache_bytes / kRowBytes;
 #pragma unroll
-        for (int k = 0; k < kRowsPer; k++) {
+        for (int k = 0; k < kRowsPer8; k++) {
             const long row = (long)pg[k] * page + (li[k] >= 0 ? li[k] % page : 0);
             const bool ok = li[k] >= 0 && pg[k] >= 0 && row < cache_rows;
-            if (tid + 256 * k < len) s_rows[tid + 256 * k] = ok ? (int)row : -1;
-            // validity of split tokens 64(4k + w) .. +63 (none past len)
+            if (tid + 512 * k < len) s_rows[tid + 512 * k] = ok ? (int)row : -1;
+            // validity of split tokens 64(8k + w) .. +63 (none past len)
             const unsigned long long m = __ballot(ok);
-            if (lane == 0) s_mask[4 * k + wave] = m;
+            if (lane == 0) s_mask[8 * k + wave] = m;
         }
     }
     lds_barrier();  // s_rows, s_mask visible (the q loads stay in flight)
 
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(cache, cache_bytes);
     // DMA: block b of a tile is filled by one instruction, lane l taking
-    // token 16 (b / 18) + (l >> 2), chunk 4 (b % 18) + ((l & 3) ^ hsw(l >> 4));
-    // wave w issues blocks w, w + 4, ..., w + 32.  The chunk-group offset goes
-    // in soffset (an instruction immediate would also move the LDS address).
-    const uint32_t lane_c16 = 16u * (uint32_t)((lane & 3) ^ hsw((lane >> 4) & 3));
-    // a token's row: its 32-bit offset (an out-of-range one reads zeros) or,
-    // WIDE, its address (the zero row for an invalid position)
+    // token 16 (b / 18) + (l >> 2), chunk 4 (b % 18) + ((l & 3) ^ ((l >> 3) & 3));
+    // the chunk-group offset goes in soffset (an instruction immediate would
+    // also move the LDS address)
+    const uint32_t lane_c16 = 16u * (uint32_t)((lane & 3) ^ ((lane >> 3) & 3));
     using RowAddr = std::conditional_t<WIDE, const uint8_t*, uint32_t>;
     auto row_vo = [&](int tok) __attribute__((always_inline)) -> RowAddr {
         if constexpr (WIDE) {
@@ -846,8 +805,10 @@ __device__ __forceinline__ void dsa_split_body(
             return vo;
         }
     };
+    // a tile's 36 blocks: wave w issues b = w + 8n, n < 5 for waves 0-3 and
+    // n < 4 for waves 4-7
     auto issue_blk = [&](int st, RowAddr vo0, RowAddr vo1, int n) __attribute__((always_inline)) {
-        const int b = wave + 4 * n;
+        const int b = wave + 8 * n;
         const int tg = b >= 18 ? 1 : 0;
         if constexpr (WIDE)
             __builtin_amdgcn_global_load_lds((gptr_t)((tg ? vo1 : vo0) + 64 * (b - 18 * tg)),
@@ -856,44 +817,12 @@ __device__ __forceinline__ void dsa_split_body(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rc, (lds_ptr_t)(smem + st * kStage32 + b * 1024), 16, tg ? vo1 : vo0, 64 * (b - 18 * tg), 0, 0);
     };
+    const bool five = wave < 4;  // uniform: this wave issues a fifth block per tile
 
-    f32x4 o[32][2];  // dims 16mt + 4g + i, head hbase + 16ht + c16
+    f32x4 o[32];  // dims 16mt + 4g + i, head hbase + c16
 #pragma unroll
-    for (int i = 0; i < 32; i++)
-        for (int j = 0; j < 2; j++) o[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // This wave's partial rows A (and spare rows B): per (query, split) H
-    // heads x 512 dims, each 16-head block stored in the accumulator order
-    // [dim tile mt][lane][4] (element (dim 16mt + 4g + i, head c16)), so a
-    // tile is one contiguous 1 KB store.
-    const size_t prow0 = ((size_t)qi * nsplit + sp) * H + hbase;
-    const size_t lane_off = (size_t)lane * 4;  // + 16 kDc ht + 256 mt
-    // O -> rows (A or B), straight from the accumulators; the base is made
-    // opaque so the addresses are formed here, not hoisted and kept live
-    auto store_o = [&](float* rows) __attribute__((always_inline)) {
-        float* base = rows + prow0 * kDc + lane_off;
-        asm volatile("" : "+v"(base));
-#pragma unroll
-        for (int ht = 0; ht < 2; ht++)
-#pragma unroll
-            for (int mt = 0; mt < 32; mt++) *(f32x4*)(base + 16 * kDc * ht + 256 * mt) = o[mt][ht];
-    };
-    // A = (first ? 0 : A) + B, times c[ht], in memory
-    auto fold_b = [&](bool first, const float (&c)[2]) __attribute__((always_inline)) {
-        float* a = part_o + prow0 * kDc + lane_off;
-        const float* b = spare_o + prow0 * kDc + lane_off;
-        asm volatile("" : "+v"(a), "+v"(b));
-#pragma unroll
-        for (int ht = 0; ht < 2; ht++)
-#pragma unroll 4
-            for (int mt = 0; mt < 32; mt++) {
-                const size_t off = 16 * kDc * ht + 256 * mt;
-                f32x4 v = *(const f32x4*)(b + off);
-                if (!first) v += *(const f32x4*)(a + off);
-                *(f32x4*)(a + off) = v * c[ht];
-            }
-    };
-    float m_run[2] = {-INFINITY, -INFINITY}, l_lane[2] = {0.f, 0.f};
-    bool flushed = false;  // uniform: part of O is in the partial rows
+    for (int i = 0; i < 32; i++) o[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_lane = 0.0f;
     const int ntiles = (len + kT32 - 1) / kT32;
 
     const int koff = tile32_off(c16, g);  // S fragment (token tile tt, K-step ks): + 1024 (18 tt + ks)
@@ -902,29 +831,31 @@ __device__ __forceinline__ void dsa_split_body(
     for (int e = 0; e < 2; e++)
         vlo[e] = tile32_off(4 * g + (c16 >> 2), 2 * e + ((c16 >> 1) & 1)) + 8 * (c16 & 1);
 
-    // prologue: tiles 0..2 (tiles past the end read zeros into their stage,
-    // so every iteration waits for the same count)
+    // prologue: tiles 0..2 (tiles past the end read zeros into their stage)
 #pragma unroll
     for (int i = 0; i < kRing32 - 1; i++) {
         const RowAddr a = row_vo(kT32 * i + (lane >> 2)), b = row_vo(kT32 * i + 16 + (lane >> 2));
 #pragma unroll
-        for (int n = 0; n < 9; n++) issue_blk(i, a, b, n);
+        for (int n = 0; n < 4; n++) issue_blk(i, a, b, n);
+        if (five) issue_blk(i, a, b, 4);
     }
     for (int t = 0; t < ntiles; t++) {
         const int tn = t + kRing32 - 1;
         const RowAddr nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
-        wait_vmcnt<9 * (kRing32 - 2)>();  // tile t landed (this wave's part)
-        bare_barrier();                   // ... everywhere; stage tn % 4 is free
+        // tile t landed (this wave's part): tiles t+1, t+2 may stay in flight
+        if (five) wait_vmcnt<10>();
+        else wait_vmcnt<8>();
+        bare_barrier();  // ... everywhere; stage tn % 4 is free
         uint32_t soff = (t % kRing32) * kStage32;
         asm volatile("" : "+s"(soff));
         const uint8_t* kb = smem + soff;
         const int stn = tn % kRing32;
 
-        // S^T, 18 K-steps; fragment reads kPre steps ahead; one load of tile
-        // tn goes out per step for the first 9
-        f32x4 sacc[2][2];
+        // S^T (2 token tiles x 16 heads), 18 K-steps; fragment reads kPre
+        // steps ahead; one block of tile tn goes out per step for the first 5
+        f32x4 sacc[2];
         {
-            constexpr int kPre = 6;
+            constexpr int kPre = 2;
             u32x4 a[18][2];
 #pragma unroll
             for (int ks = 0; ks < kPre; ks++)
@@ -936,70 +867,54 @@ __device__ __forceinline__ void dsa_split_body(
 #pragma unroll
                     for (int tt = 0; tt < 2; tt++)
                         a[ks + kPre][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks + kPre));
-                s_mfma4<ks == 0, ks == 17>(sacc, a[ks][0], a[ks][1], qf[0][ks], qf[1][ks]);
-                if (ks < 9) issue_blk(stn, nvo0, nvo1, ks);
-                // keep the prefetch depth as written: with O and q resident,
-                // hoisted fragment reads would spill
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+                    sacc[tt] = mfma_bf16(a[ks][tt], qf[ks], ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sacc[tt]);
+                if constexpr (ks < 4) issue_blk(stn, nvo0, nvo1, ks);
+                if constexpr (ks == 4)
+                    if (five) issue_blk(stn, nvo0, nvo1, 4);
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
-        // lane: head 16ht + c16, tokens 16tt + 4g + i of the tile; an
-        // invalid token (or one past the split) scores -inf
-        float sv[2][2][4], tm[2];
+        // lane: head c16, tokens 16tt + 4g + i of the tile; an invalid token
+        // (or one past the split) scores -inf
+        float sv[2][4], tm = -INFINITY;
         const uint32_t vmask = (uint32_t)(s_mask[t >> 1] >> (32 * (t & 1) + 4 * g));
 #pragma unroll
-        for (int ht = 0; ht < 2; ht++) {
-            tm[ht] = -INFINITY;
+        for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    sv[tt][ht][i] = (vmask >> (16 * tt + i)) & 1u ? sacc[tt][ht][i] * scale_log2 : -INFINITY;
-                    tm[ht] = fmaxf(tm[ht], sv[tt][ht][i]);
-                }
-            tm[ht] = xor32_max(xor16_max(tm[ht]));
-        }
-        // uniform: no valid token so far (validity is per token, the same
-        // for every head, so all heads' maxima are finite or none is)
-        const bool first = m_run[0] == -INFINITY;
-        const bool raise = tm[0] > m_run[0] + 8.0f || tm[1] > m_run[1] + 8.0f;
-        if (first) {
-            m_run[0] = tm[0];
-            m_run[1] = tm[1];
-        } else if (__ballot(raise)) {
-            // rare: A = (A + O) scaled to the new max, O restarts at zero
-            float corr[2];
-#pragma unroll
-            for (int ht = 0; ht < 2; ht++) {
-                const float m_new = fmaxf(m_run[ht], tm[ht]);
-                corr[ht] = exp2f(m_run[ht] - m_new);
-                l_lane[ht] *= corr[ht];
-                m_run[ht] = m_new;
+            for (int i = 0; i < 4; i++) {
+                sv[tt][i] = (vmask >> (16 * tt + i)) & 1u ? sacc[tt][i] * scale_log2 : -INFINITY;
+                tm = fmaxf(tm, sv[tt][i]);
             }
-            store_o(spare_o);
-            fold_b(!flushed, corr);
+        tm = xor32_max(xor16_max(tm));
+        // uniform: no valid token so far (validity is per token, the same
+        // for every head)
+        if (m_run == -INFINITY) {
+            m_run = tm;
+        } else if (__ballot(tm > m_run + 8.0f)) {
+            // rare: rescale O and l to a new running max
+            const float m_new = fmaxf(m_run, tm);
+            const float corr = exp2f(m_run - m_new);
+            l_lane *= corr;
+            m_run = m_new;
 #pragma unroll
-            for (int ht = 0; ht < 2; ht++)
-#pragma unroll
-                for (int mt = 0; mt < 32; mt++) o[mt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            flushed = true;
+            for (int mt = 0; mt < 32; mt++) o[mt] *= corr;
         }
-        u32x4 pb[2];
-#pragma unroll
-        for (int ht = 0; ht < 2; ht++) {
+        u32x4 pb;
+        {
             float p[2][4];
             // with no valid token yet every score is -inf: subtract 0, not -inf
-            const float m_use = m_run[ht] == -INFINITY ? 0.0f : m_run[ht];
+            const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    // the hardware exp2 (0 for a masked -inf score)
-                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][ht][i] - m_use);
-                    l_lane[ht] += p[tt][i];
+                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - m_use);  // 0 for a masked -inf score
+                    l_lane += p[tt][i];
                 }
-            pb[ht] = (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
-                             pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+            pb = (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                         pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
         }
         auto vfrag = [&](int mt) __attribute__((always_inline)) {
             const uint8_t* p = kb + vlo[mt & 1] + 1024 * (mt >> 1);
@@ -1008,61 +923,39 @@ __device__ __forceinline__ void dsa_split_body(
             const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
             return (u32x4){l2[0], l2[1], h2[0], h2[1]};
         };
-        constexpr int kPreV = 10;
+        constexpr int kPreV = 6;
         u32x4 va[32];
 #pragma unroll
         for (int mt = 0; mt < kPreV; mt++) va[mt] = vfrag(mt);
 #pragma unroll
         for (int mt = 0; mt < 32; mt++) {
             if (mt + kPreV < 32) va[mt + kPreV] = vfrag(mt + kPreV);
-            o[mt][0] = mfma_bf16(va[mt], pb[0], o[mt][0]);
-            o[mt][1] = mfma_bf16(va[mt], pb[1], o[mt][1]);
+            o[mt] = mfma_bf16(va[mt], pb, o[mt]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     wait_vmcnt<0>();  // the trailing (out-of-range) tile loads
 
     // the split's partial, bf16 in the accumulator order (512 contiguous
-    // bytes per store): O, or, if part of O was flushed, A + O
-    uint16_t* pb_base = part_b + prow0 * kDc + lane_off;
-    asm volatile("" : "+v"(pb_base));
-    if (!flushed) {
+    // bytes per store), and (max, sum) per head
+    const size_t prow0 = ((size_t)qi * nsplit + sp) * H + hbase;
+    uint16_t* pb_base = part_b + prow0 * kDc + (size_t)lane * 4;
 #pragma unroll
-        for (int ht = 0; ht < 2; ht++)
-#pragma unroll
-            for (int mt = 0; mt < 32; mt++)
-                *(u32x2*)(pb_base + 16 * kDc * ht + 256 * mt) =
-                    (u32x2){pack_bf16x2(o[mt][ht][0], o[mt][ht][1]), pack_bf16x2(o[mt][ht][2], o[mt][ht][3])};
-    } else {
-        store_o(spare_o);
-        const float one[2] = {1.0f, 1.0f};
-        fold_b(false, one);
-        const float* a = part_o + prow0 * kDc + lane_off;
-#pragma unroll
-        for (int ht = 0; ht < 2; ht++)
-#pragma unroll 4
-            for (int mt = 0; mt < 32; mt++) {
-                const size_t off = 16 * kDc * ht + 256 * mt;
-                const f32x4 v = *(const f32x4*)(a + off);
-                *(u32x2*)(pb_base + off) = (u32x2){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            }
-    }
-#pragma unroll
-    for (int ht = 0; ht < 2; ht++) {
-        const float l = xor32_sum(xor16_sum(l_lane[ht]));
-        if (g == 0) *(float2*)(part_ml + 2 * (prow0 + 16 * ht + c16)) = make_float2(m_run[ht], l);
-    }
+    for (int mt = 0; mt < 32; mt++)
+        *(u32x2*)(pb_base + 256 * mt) =
+            (u32x2){pack_bf16x2(o[mt][0], o[mt][1]), pack_bf16x2(o[mt][2], o[mt][3])};
+    const float l = xor32_sum(xor16_sum(l_lane));
+    if (g == 0) *(float2*)(part_ml + 2 * (prow0 + c16)) = make_float2(m_run, l);
 }
 
-#define AMDMOE_DSA_SPLIT_KERNEL(NAME, W)                                                              \
-    __global__ __launch_bounds__(256, 1) void NAME(                                                   \
+#define AMDMOE_DSA_SPLIT_KERNEL(NAME, W)                                                             \
+    __global__ __launch_bounds__(512, 1) void NAME(                                                   \
         const uint16_t* __restrict__ qn, const uint16_t* __restrict__ qp,                             \
         const uint16_t* __restrict__ cache, long cache_bytes, const int* __restrict__ page_table,     \
-        const int* __restrict__ logical, float* __restrict__ part_o, float* __restrict__ spare_o,     \
-        uint16_t* __restrict__ part_b, float* __restrict__ part_ml, int Q, int H, int S, int page,    \
-        int pages_per_seq, int nsplit, int chunk, float scale_log2) {                                 \
-        dsa_split_body<W>(qn, qp, cache, cache_bytes, page_table, logical, part_o, spare_o, part_b,   \
-                          part_ml, Q, H, S, page, pages_per_seq, nsplit, chunk, scale_log2);          \
+        const int* __restrict__ logical, uint16_t* __restrict__ part_b, float* __restrict__ part_ml,  \
+        int Q, int H, int S, int page, int pages_per_seq, int nsplit, int chunk, float scale_log2) {  \
+        dsa_split_body<W>(qn, qp, cache, cache_bytes, page_table, logical, part_b, part_ml, Q, H, S, \
+                           page, pages_per_seq, nsplit, chunk, scale_log2);                           \
     }
 AMDMOE_DSA_SPLIT_KERNEL(dsa_split_kernel, false)
 AMDMOE_DSA_SPLIT_KERNEL(dsa_split_wide_kernel, true)
@@ -1132,8 +1025,8 @@ static int dsa_nsplit(int Q, int H, int S) {
 size_t dsa_paged_scratch_bytes(int Q, int H, int S) {
     if (Q <= 0 || H % 128 != 0 || S < 1) return 0;  // the kernels without splits
     const size_t rows = (size_t)Q * dsa_nsplit(Q, H, S) * H;
-    // rows A, spare rows B (fp32), the bf16 partials, (m, l)
-    return 2 * rows * kDc * 4 + rows * kDc * 2 + align_up(rows * 8, 256);
+    // the bf16 partials, (m, l)
+    return align_up(rows * kDc * 2, 256) + align_up(rows * 8, 256);
 }
 
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
@@ -1164,17 +1057,14 @@ int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t
                          "dsa_decode_bf16_paged: scratch of %zu bytes, %zu needed", scratch_bytes, need);
         const long grid = ceil_div((long)Q * (H / 128) * ns, 8) * 8;
         AMDMOE_CHECK_ARG(grid < (1L << 31), "dsa_decode_bf16_paged: grid too large");
-        const size_t rows_bytes = (size_t)Q * ns * H * kDc * 4;
-        float* part_o = (float*)scratch;
-        float* spare_o = (float*)((uint8_t*)scratch + rows_bytes);
-        uint16_t* part_b = (uint16_t*)((uint8_t*)scratch + 2 * rows_bytes);
-        float* part_ml = (float*)((uint8_t*)scratch + 2 * rows_bytes + rows_bytes / 2);
+        uint16_t* part_b = (uint16_t*)scratch;
+        float* part_ml = (float*)((uint8_t*)scratch + align_up((size_t)Q * ns * H * kDc * 2, 256));
         auto split = wide ? dsa_split_wide_kernel : dsa_split_kernel;
         const int rc = ensure_dynamic_lds((const void*)split, kDsaSplitLds);
         if (rc != AMDMOE_OK) return rc;
-        hipLaunchKernelGGL(split, dim3((unsigned)grid), dim3(256), kDsaSplitLds, st, qn,
-                           qp, cache, cache_tokens * kRowBytes, page_table, logical, part_o, spare_o,
-                           part_b, part_ml, Q, H, S, page, pages_per_seq, ns, chunk, scale_log2);
+        hipLaunchKernelGGL(split, dim3((unsigned)grid), dim3(512), kDsaSplitLds, st, qn, qp, cache,
+                           cache_tokens * kRowBytes, page_table, logical, part_b, part_ml, Q, H, S, page,
+                           pages_per_seq, ns, chunk, scale_log2);
         AMDMOE_LAUNCH_CHECK();
         hipLaunchKernelGGL(dsa_merge_kernel, dim3((unsigned)(ceil_div((long)Q * (H / 16), 8) * 8)),
                            dim3(256), 0, st, (const uint16_t*)part_b, (const float*)part_ml, out, Q, H, ns);
