@@ -647,8 +647,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bf16_paged64_kernel(
 // group for all of the split's tokens, so its softmax state is private (no
 // exchange between waves) and P goes from the S^T accumulators straight
 // into the PV MFMA operand.  32-token tiles stream through a 4-stage LDS
-// ring (three tiles in flight), filled by direct global->LDS loads; each
-// wave reads every tile once for S and once for V.
+// ring (each tile's loads go out two tiles ahead), filled by direct
+// global->LDS loads; each wave reads every tile once for S and once for V.
 //   S^T (16 tokens x 16 heads) = K . Q^T   16x16x32 bf16, 2 token tiles,
 //                                          q of the wave's 16 heads in
 //                                          registers
@@ -831,53 +831,62 @@ __device__ __forceinline__ void dsa_split_body(
     for (int e = 0; e < 2; e++)
         vlo[e] = tile32_off(4 * g + (c16 >> 2), 2 * e + ((c16 >> 1) & 1)) + 8 * (c16 & 1);
 
-    // prologue: tiles 0..2 (tiles past the end read zeros into their stage)
+    // The two waves of a SIMD (w and w + 4) run half a tile apart: waves
+    // 0-3 pass the tile barrier at the start of a tile, waves 4-7 between
+    // their S^T and PV phases, so one wave's S^T fragment reads, softmax and
+    // barrier wait run under the other's PV MFMAs.  Barrier n is where waves
+    // 0-3 start tile n and waves 4-7 finish S^T of tile n-1, so tile n's
+    // stage is read between barriers n and n+2; the DMA of tile n+2 goes out
+    // after barrier n into the stage of tile n-2 (read until barrier n), and
+    // every wave waits for its blocks of tile n before barrier n.  Each wave
+    // passes ntiles + 1 barriers.
+    const bool lag = wave >= 4;  // uniform
+    // prologue: tiles 0 and 1 (tiles past the end read zeros into their stage)
 #pragma unroll
-    for (int i = 0; i < kRing32 - 1; i++) {
+    for (int i = 0; i < 2; i++) {
         const RowAddr a = row_vo(kT32 * i + (lane >> 2)), b = row_vo(kT32 * i + 16 + (lane >> 2));
 #pragma unroll
         for (int n = 0; n < 4; n++) issue_blk(i, a, b, n);
         if (five) issue_blk(i, a, b, 4);
     }
-    for (int t = 0; t < ntiles; t++) {
-        const int tn = t + kRing32 - 1;
-        const RowAddr nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
-        // tile t landed (this wave's part): tiles t+1, t+2 may stay in flight
-        if (five) wait_vmcnt<10>();
-        else wait_vmcnt<8>();
-        bare_barrier();  // ... everywhere; stage tn % 4 is free
-        uint32_t soff = (t % kRing32) * kStage32;
-        asm volatile("" : "+s"(soff));
-        const uint8_t* kb = smem + soff;
-        const int stn = tn % kRing32;
+    // this wave's blocks of the older of its two tiles in flight have landed
+    auto wait_older = [&]() __attribute__((always_inline)) {
+        if (five) wait_vmcnt<5>();
+        else wait_vmcnt<4>();
+    };
 
-        // S^T (2 token tiles x 16 heads), 18 K-steps; fragment reads kPre
-        // steps ahead; one block of tile tn goes out per step for the first 5
-        f32x4 sacc[2];
-        {
-            constexpr int kPre = 2;
-            u32x4 a[18][2];
+    // S^T (2 token tiles x 16 heads) of the tile in stage soff, 18 K-steps,
+    // fragment reads kPre steps ahead; with ISSUE, one block of tile tn goes
+    // out per step for the first 5
+    auto s_phase = [&](auto issuec, uint32_t soff, int stn, RowAddr nvo0, RowAddr nvo1,
+                       f32x4 (&sacc)[2]) __attribute__((always_inline)) {
+        constexpr bool ISSUE = decltype(issuec)::value;
+        const uint8_t* kb = smem + soff;
+        constexpr int kPre = 2;
+        u32x4 a[18][2];
 #pragma unroll
-            for (int ks = 0; ks < kPre; ks++)
+        for (int ks = 0; ks < kPre; ks++)
 #pragma unroll
-                for (int tt = 0; tt < 2; tt++) a[ks][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks));
-            static_for<18>([&](auto ksc) __attribute__((always_inline)) {
-                constexpr int ks = decltype(ksc)::value;
-                if constexpr (ks + kPre < 18)
-#pragma unroll
-                    for (int tt = 0; tt < 2; tt++)
-                        a[ks + kPre][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks + kPre));
+            for (int tt = 0; tt < 2; tt++) a[ks][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks));
+        static_for<18>([&](auto ksc) __attribute__((always_inline)) {
+            constexpr int ks = decltype(ksc)::value;
+            if constexpr (ks + kPre < 18)
 #pragma unroll
                 for (int tt = 0; tt < 2; tt++)
-                    sacc[tt] = mfma_bf16(a[ks][tt], qf[ks], ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sacc[tt]);
-                if constexpr (ks < 4) issue_blk(stn, nvo0, nvo1, ks);
-                if constexpr (ks == 4)
-                    if (five) issue_blk(stn, nvo0, nvo1, 4);
-                __builtin_amdgcn_sched_barrier(0);
-            });
-        }
-        // lane: head c16, tokens 16tt + 4g + i of the tile; an invalid token
-        // (or one past the split) scores -inf
+                    a[ks + kPre][tt] = *(const u32x4*)(kb + koff + 1024 * (18 * tt + ks + kPre));
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+                sacc[tt] = mfma_bf16(a[ks][tt], qf[ks], ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sacc[tt]);
+            if constexpr (ISSUE && ks < 4) issue_blk(stn, nvo0, nvo1, ks);
+            if constexpr (ISSUE && ks == 4)
+                if (five) issue_blk(stn, nvo0, nvo1, 4);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    // online softmax of tile t's scores; returns P^T as the PV B operand.
+    // Lane: head c16, tokens 16tt + 4g + i of the tile; an invalid token (or
+    // one past the split) scores -inf
+    auto softmax = [&](int t, const f32x4 (&sacc)[2]) __attribute__((always_inline)) -> u32x4 {
         float sv[2][4], tm = -INFINITY;
         const uint32_t vmask = (uint32_t)(s_mask[t >> 1] >> (32 * (t & 1) + 4 * g));
 #pragma unroll
@@ -901,21 +910,25 @@ __device__ __forceinline__ void dsa_split_body(
 #pragma unroll
             for (int mt = 0; mt < 32; mt++) o[mt] *= corr;
         }
-        u32x4 pb;
-        {
-            float p[2][4];
-            // with no valid token yet every score is -inf: subtract 0, not -inf
-            const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        float p[2][4];
+        // with no valid token yet every score is -inf: subtract 0, not -inf
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++)
+        for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - m_use);  // 0 for a masked -inf score
-                    l_lane += p[tt][i];
-                }
-            pb = (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
-                         pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-        }
+            for (int i = 0; i < 4; i++) {
+                p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - m_use);  // 0 for a masked -inf score
+                l_lane += p[tt][i];
+            }
+        return (u32x4){pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                       pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+    };
+    // O^T += V^T . P^T over the tile in stage soff; with ISSUE, one block of
+    // tile tn goes out after each of the first 5 dim tiles
+    auto pv_phase = [&](auto issuec, uint32_t soff, int stn, RowAddr nvo0, RowAddr nvo1,
+                        const u32x4& pb) __attribute__((always_inline)) {
+        constexpr bool ISSUE = decltype(issuec)::value;
+        const uint8_t* kb = smem + soff;
         auto vfrag = [&](int mt) __attribute__((always_inline)) {
             const uint8_t* p = kb + vlo[mt & 1] + 1024 * (mt >> 1);
             const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)p);
@@ -927,11 +940,59 @@ __device__ __forceinline__ void dsa_split_body(
         u32x4 va[32];
 #pragma unroll
         for (int mt = 0; mt < kPreV; mt++) va[mt] = vfrag(mt);
-#pragma unroll
-        for (int mt = 0; mt < 32; mt++) {
-            if (mt + kPreV < 32) va[mt + kPreV] = vfrag(mt + kPreV);
+        static_for<32>([&](auto mtc) __attribute__((always_inline)) {
+            constexpr int mt = decltype(mtc)::value;
+            if constexpr (mt + kPreV < 32) va[mt + kPreV] = vfrag(mt + kPreV);
             o[mt] = mfma_bf16(va[mt], pb, o[mt]);
+            if constexpr (ISSUE && mt < 4) issue_blk(stn, nvo0, nvo1, mt);
+            if constexpr (ISSUE && mt == 4)
+                if (five) issue_blk(stn, nvo0, nvo1, 4);
             __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    auto stage_of = [](int t) __attribute__((always_inline)) -> uint32_t {
+        uint32_t soff = (uint32_t)(t % kRing32) * kStage32;
+        asm volatile("" : "+s"(soff));
+        return soff;
+    };
+    using on = std::integral_constant<bool, true>;
+    using off = std::integral_constant<bool, false>;
+
+    if (!lag) {
+        // the q loads (older than the tile DMA) have landed: without this the
+        // compiler waits for every load in flight, tile 1's included
+        wait_older();
+        for (int t = 0; t < ntiles; t++) {
+            const int tn = t + 2;
+            const RowAddr nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
+            wait_older();    // tile t landed (this wave's part); tile t+1 may stay in flight
+            bare_barrier();  // barrier t
+            const uint32_t soff = stage_of(t);
+            f32x4 sacc[2];
+            s_phase(on{}, soff, tn % kRing32, nvo0, nvo1, sacc);
+            const u32x4 pb = softmax(t, sacc);
+            pv_phase(off{}, soff, 0, nvo0, nvo1, pb);
+        }
+        bare_barrier();  // barrier ntiles
+    } else {
+        wait_older();
+        bare_barrier();  // barrier 0
+        {
+            const RowAddr a = row_vo(kT32 * 2 + (lane >> 2)), b = row_vo(kT32 * 2 + 16 + (lane >> 2));
+#pragma unroll
+            for (int n = 0; n < 4; n++) issue_blk(2, a, b, n);
+            if (five) issue_blk(2, a, b, 4);
+        }
+        for (int t = 0; t < ntiles; t++) {
+            const int tn = t + 3;
+            const RowAddr nvo0 = row_vo(kT32 * tn + (lane >> 2)), nvo1 = row_vo(kT32 * tn + 16 + (lane >> 2));
+            const uint32_t soff = stage_of(t);
+            f32x4 sacc[2];
+            s_phase(off{}, soff, 0, nvo0, nvo1, sacc);
+            const u32x4 pb = softmax(t, sacc);
+            wait_older();    // tile t+1 landed (this wave's part); tile t+2 may stay in flight
+            bare_barrier();  // barrier t+1
+            pv_phase(on{}, soff, tn % kRing32, nvo0, nvo1, pb);
         }
     }
     wait_vmcnt<0>();  // the trailing (out-of-range) tile loads
@@ -966,6 +1027,9 @@ AMDMOE_DSA_SPLIT_KERNEL(dsa_split_wide_kernel, true)
 // (sum c_j l_j), bf16.  Workgroup = one query x 16 heads (one partial block),
 // wave w = dim tiles 8w..8w+7 in the block's accumulator order: every load
 // is 512 bytes contiguous, and lane (g, c) holds dims 16mt + 4g + i of head c.
+// Splits are read four at a time, every load of the four in flight at once
+// (one round trip for up to four splits); a later group whose maximum is
+// higher rescales the sums so far by 2^(m_old - m_new).
 __global__ __launch_bounds__(256) void dsa_merge_kernel(const uint16_t* __restrict__ part_b,
                                                         const float* __restrict__ part_ml,
                                                         uint16_t* __restrict__ out, int Q,
@@ -980,27 +1044,45 @@ __global__ __launch_bounds__(256) void dsa_merge_kernel(const uint16_t* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int h = 16 * hb + c16;
-    float m = -INFINITY;
-    for (int j = 0; j < nsplit; j++) m = fmaxf(m, part_ml[2 * (((size_t)qi * nsplit + j) * H + h)]);
+    constexpr int kGroup = 4;
     f32x4 acc[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) acc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float L = 0.0f;
-    for (int j = 0; j < nsplit; j++) {
-        const size_t blk = ((size_t)qi * nsplit + j) * H + 16 * hb;  // first row of the block
-        const float2 ml = *(const float2*)(part_ml + 2 * (blk + c16));
-        const float c = ml.x == -INFINITY ? 0.0f : exp2f(ml.x - m);
-        L += c * ml.y;
-        const u32x2* po = (const u32x2*)(part_b + blk * kDc) + 64 * 8 * wave + lane;
-        u32x2 pv[8];
+    float m = -INFINITY, L = 0.0f;
+    for (int j0 = 0; j0 < nsplit; j0 += kGroup) {
+        float2 ml[kGroup];
+        u32x2 pv[kGroup][8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) pv[k] = po[64 * k];
+        for (int u = 0; u < kGroup; u++) {
+            const int j = min(j0 + u, nsplit - 1);  // in bounds; splits past the end get weight 0
+            const size_t blk = ((size_t)qi * nsplit + j) * H + 16 * hb;  // first row of the block
+            ml[u] = *(const float2*)(part_ml + 2 * (blk + c16));
+            const u32x2* po = (const u32x2*)(part_b + blk * kDc) + 64 * 8 * wave + lane;
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            acc[k][0] += c * __uint_as_float(pv[k][0] << 16);
-            acc[k][1] += c * __uint_as_float(pv[k][0] & 0xffff0000u);
-            acc[k][2] += c * __uint_as_float(pv[k][1] << 16);
-            acc[k][3] += c * __uint_as_float(pv[k][1] & 0xffff0000u);
+            for (int k = 0; k < 8; k++) pv[u][k] = po[64 * k];
+        }
+        float mg = m;
+#pragma unroll
+        for (int u = 0; u < kGroup; u++)
+            if (j0 + u < nsplit) mg = fmaxf(mg, ml[u].x);
+        if (mg == -INFINITY) continue;  // no valid position so far: the sums stay 0
+        // the sums so far are 0 while m = -inf
+        const float r = m == -INFINITY ? 0.0f : exp2f(m - mg);
+        L *= r;
+#pragma unroll
+        for (int k = 0; k < 8; k++) acc[k] *= r;
+        m = mg;
+#pragma unroll
+        for (int u = 0; u < kGroup; u++) {
+            const float c = j0 + u < nsplit && ml[u].x != -INFINITY ? exp2f(ml[u].x - m) : 0.0f;
+            L += c * ml[u].y;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc[k][0] += c * __uint_as_float(pv[u][k][0] << 16);
+                acc[k][1] += c * __uint_as_float(pv[u][k][0] & 0xffff0000u);
+                acc[k][2] += c * __uint_as_float(pv[u][k][1] << 16);
+                acc[k][3] += c * __uint_as_float(pv[u][k][1] & 0xffff0000u);
+            }
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
