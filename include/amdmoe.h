@@ -19,9 +19,10 @@
  *     share one workspace must be ordered on one stream.
  *   - Entry points without a workspace argument that need scratch (the
  *     split-K routing of amdmoe_moe_gate_bf16/_fp8, amdmoe_moe_permute,
- *     amdmoe_dsa_decode_bf16_paged, amdmoe_dsa_forward_f32 with S > 16384)
+ *     amdmoe_dsa_decode_bf16_paged, amdmoe_dsa_forward_f32 with S > 16384,
+ *     amdmoe_dsa_indexer_topk_fp8 selecting in parts)
  *     use a per-device buffer of their own family (routing, permutation,
- *     decode, fp32 DSA; none is shared with the MoE forward's workspace or
+ *     decode, fp32 DSA, indexer; none is shared with the MoE forward's workspace or
  *     with another family).  A call that must grow that buffer frees and
  *     allocates it, which waits for the device; calls of one family that use
  *     the buffer must be ordered on one stream (concurrent calls of one
@@ -338,7 +339,12 @@ int amdmoe_dsa_decode_bf16_paged(const uint16_t* q_nope, const uint16_t* q_pe,
  * scores (ties: the lower position), in ascending position order; a query
  * with fewer than topk positions lists all of them, then -1.  scores fp32
  * [Q, max_seq] is caller scratch (left holding the scores, -inf past
- * seq_len).  Hi in {16, 32, 64, 128}; max_seq <= 32768. */
+ * seq_len).  Hi in {16, 32, 64, 128}; max_seq <= 131072, and above 32768
+ * only while the row splits into parts of at most 32768 positions, each
+ * longer than topk, with parts * topk <= 32768.  Rows are selected in parts
+ * when that fills the device (few queries) or the row is long; the parts'
+ * candidates then live in the indexer's own per-device scratch (see the
+ * scratch rules above). */
 int amdmoe_dsa_indexer_topk_fp8(const uint8_t* q_codes, const float* q_scale, const float* head_w,
                                 const uint8_t* k_codes, const float* k_scale, long cache_rows,
                                 const int* page_table, const int* seq_len, int num_queries,

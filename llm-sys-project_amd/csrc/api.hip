@@ -105,7 +105,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
 // never share memory.  Calls of one family that use it must be ordered on
 // one stream; the call that grows a buffer frees and allocates (hipFree
 // waits for the device).
-enum ScratchKind { SCR_MOE = 0, SCR_GATE, SCR_PERMUTE, SCR_DSA_DECODE, SCR_DSA_F32, SCR_KINDS };
+enum ScratchKind { SCR_MOE = 0, SCR_GATE, SCR_PERMUTE, SCR_DSA_DECODE, SCR_DSA_F32, SCR_DSA_INDEXER, SCR_KINDS };
 struct CachedWs {
     std::mutex m;
     void* ptr = nullptr;
@@ -646,9 +646,13 @@ int amdmoe_dsa_indexer_topk_fp8(const uint8_t* q_codes, const float* q_scale, co
     AMDMOE_CHECK_ARG(q_codes && q_scale && head_w && k_codes && k_scale && page_table && seq_len &&
                          scores && out,
                      "null tensor pointer");
+    // the two-stage selection's candidates live in the indexer's own cached scratch
+    const size_t need = dsa_indexer_scratch_bytes(num_queries, max_seq, topk);
+    void* scratch = nullptr;
+    if (need) TRY(cached_workspace(need, &scratch, SCR_DSA_INDEXER));
     return launch_dsa_indexer(q_codes, q_scale, head_w, k_codes, cache_rows, k_scale, page_table,
                               seq_len, num_queries, num_heads, page, pages_per_seq, max_seq, topk,
-                              scores, out, (hipStream_t)stream);
+                              scores, out, scratch, need, (hipStream_t)stream);
 }
 
 int amdmoe_dsa_kv_gather_f32(const float* kv_cache_compressed, const float* kv_cache_positional,

@@ -43,7 +43,8 @@ namespace amdmoe {
 constexpr int kIdxD = 128;         // index head dim (bytes per fp8 row)
 constexpr int kIdxMaxHeads = 128;  // index heads, a multiple of 16
 constexpr int kIdxTile = 256;      // positions per workgroup of the scoring kernel
-constexpr int kIdxMaxSeq = 32768;  // positions per query of the selection kernel
+constexpr int kIdxMaxSeq = 32768;  // keys one selection workgroup holds (1024 threads x 32)
+constexpr int kIdxMaxRow = 4 * kIdxMaxSeq;  // positions per query (rows above kIdxMaxSeq in parts)
 constexpr int kTopkThreads = 1024;
 
 // position -> (page, slot): shifts when the page size is a power of two
@@ -198,33 +199,73 @@ __device__ __forceinline__ int count_below(unsigned long long m) {
     return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
 }
 
-template <int kPer>  // positions per thread: max_seq <= 1024 * kPer
+// Selection modes: FULL selects a query's row in one workgroup; PART
+// selects within one of the row's parts (positions [part * chunk, +chunk))
+// and writes its top-k as (key, position) candidates in position order,
+// padded with position -1; MERGE selects over a query's parts' candidates,
+// read in part order, i.e. in position order.  Every position of the global
+// top-k is in its part's top-k (the same order: key, then lower position),
+// so PART + MERGE select exactly what FULL does.
+enum { kSelFull = 0, kSelPart = 1, kSelMerge = 2 };
+
+template <int kPer, int MODE>  // keys per thread: 1024 * kPer >= the keys one workgroup selects from
 __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float* __restrict__ scores,
                                                                     const int* __restrict__ seq_len,
                                                                     int max_seq, int cap, int topk,
+                                                                    int nparts, int chunk,
+                                                                    uint2* __restrict__ cand,
                                                                     int* __restrict__ out) {
     constexpr int kWaves = kTopkThreads / 64;
     __shared__ __align__(16) int s_hist[kWaves][256];  // one histogram per wave
     __shared__ unsigned s_slice[kPer + 1];             // counts before each slice, total
     __shared__ int s_sel[2];                           // digit, remaining count
-    const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int s_nvalid;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qi = MODE == kSelPart ? blockIdx.x / nparts : blockIdx.x;
+    const int part = MODE == kSelPart ? blockIdx.x - qi * nparts : 0;
     // the positions the scoring kernel scored: seq_len, at most max_seq
     // and the page-table row's capacity (cap = min of the two)
     const int n = max(0, min(seq_len[qi], cap));
     const float* row = scores + (size_t)qi * max_seq;
-    // histogram passes: position j * 1024 + tid in key[j], so the 64 lanes
-    // of a wave hold 64 unrelated positions
+    // key j of this thread is slot j * 1024 + tid of the workgroup's range
+    // (positions, or candidates in MERGE), so the 64 lanes of a wave hold 64
+    // unrelated slots; pos[j] is its position, -1 when it selects nothing
     uint32_t key[kPer];
+    int pos[kPer];
+    int nvalid;
+    if constexpr (MODE == kSelMerge) {
+        const uint2* cq = cand + (size_t)qi * nparts * topk;
+        int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < kPer; j++) {
-        const int s = j * kTopkThreads + tid;
-        key[j] = s < n ? score_key(row[s]) : 0u;
+        for (int j = 0; j < kPer; j++) {
+            const int c = j * kTopkThreads + tid;
+            const uint2 v = c < nparts * topk ? cq[c] : make_uint2(0u, 0xffffffffu);
+            key[j] = v.x;
+            pos[j] = (int)v.y;
+            cnt += __popcll(__ballot(pos[j] >= 0));
+        }
+        if (tid == 0) s_nvalid = 0;
+        __syncthreads();
+        if (lane == 0) atomicAdd(&s_nvalid, cnt);
+        __syncthreads();
+        nvalid = s_nvalid;
+    } else {
+        const int lo = MODE == kSelPart ? part * chunk : 0;
+        const int hi = MODE == kSelPart ? min(n, lo + chunk) : n;
+        nvalid = max(0, hi - lo);
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const int s = lo + j * kTopkThreads + tid;
+            const bool v = s < hi;
+            key[j] = v ? score_key(row[s]) : 0u;
+            pos[j] = v ? s : -1;
+        }
     }
 
-    // radix select of the topk-th largest key among the n valid positions
+    // radix select of the topk-th largest key among the valid slots
     uint32_t prefix = 0, mask = 0;
-    int need = min(topk, n);
-    const bool all = n <= topk;
+    int need = min(topk, nvalid);
+    const bool all = nvalid <= topk;
     if (!all) {
         for (int i = tid; i < kWaves * 256; i += kTopkThreads) (&s_hist[0][0])[i] = 0;
         __syncthreads();
@@ -232,7 +273,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
 #pragma unroll
             for (int j = 0; j < kPer; j++) {
                 const int d = (key[j] >> shift) & 0xff;
-                bool pending = j * kTopkThreads + tid < n && (key[j] & mask) == prefix;
+                bool pending = pos[j] >= 0 && (key[j] & mask) == prefix;
                 if (shift == 24) {
                     // leading digits cluster (sign and high exponent bits):
                     // the lanes sharing the first pending lane's digit add
@@ -292,16 +333,15 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
             need = s_sel[1];
         }
     }
-    // prefix = the threshold key; positions above it are all taken, and the
-    // first `need` positions equal to it.  Slice j of the row (positions
-    // j * 1024 + tid) is in position order across the workgroup, so each
-    // position's output slot is the greater / equal keys of the slices
-    // before it, of the waves before it in its slice (LDS counts) and of the
-    // lanes below it (ballots).
+    // prefix = the threshold key; slots above it are all taken, and the
+    // first `need` slots equal to it.  Slice j (slots j * 1024 + tid) is in
+    // slot order across the workgroup, so each slot's output position is the
+    // greater / equal keys of the slices before it, of the waves before it in
+    // its slice (LDS counts) and of the lanes below it (ballots).
     unsigned* s_cnt = (unsigned*)&s_hist[0][0];  // [wave][slice]: greater | equal << 16
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
-        const bool valid = j * kTopkThreads + tid < n;
+        const bool valid = pos[j] >= 0;
         const unsigned long long gm = __ballot(valid && (all || key[j] > prefix));
         const unsigned long long em = __ballot(valid && !all && key[j] == prefix);
         if (lane == 0) s_cnt[wave * kPer + j] = (unsigned)__popcll(gm) | ((unsigned)__popcll(em) << 16);
@@ -309,7 +349,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     __syncthreads();
     if (wave == 0) {
         // counts before each (wave, slice) within the slice, in place, then
-        // before each slice (both halves stay below 2^16: n <= 32768)
+        // before each slice (both halves stay below 2^16: at most 32768 slots)
         unsigned run = 0;
         if (lane < kPer)
             for (int w = 0; w < kWaves; w++) {
@@ -328,19 +368,46 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     }
     __syncthreads();
     int* o = out + (size_t)qi * topk;
+    uint2* cp = cand + ((size_t)qi * nparts + part) * topk;
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
-        const int s = j * kTopkThreads + tid;
-        const bool valid = s < n;
+        const bool valid = pos[j] >= 0;
         const bool gt = valid && (all || key[j] > prefix), eq = valid && !all && key[j] == prefix;
         const unsigned long long gm = __ballot(gt), em = __ballot(eq);
         const unsigned base = s_slice[j] + s_cnt[wave * kPer + j];
         const int gb = (int)(base & 0xffff) + count_below(gm), eb = (int)(base >> 16) + count_below(em);
-        if (gt || (eq && eb < need)) o[gb + min(eb, need)] = s;
+        if (gt || (eq && eb < need)) {
+            if constexpr (MODE == kSelPart) cp[gb + min(eb, need)] = make_uint2(key[j], (uint32_t)pos[j]);
+            else o[gb + min(eb, need)] = pos[j];
+        }
     }
     const unsigned tot = s_slice[kPer];
     const int total = (int)(tot & 0xffff) + min((int)(tot >> 16), need);
-    for (int j = total + tid; j < topk; j += kTopkThreads) o[j] = -1;
+    for (int j = total + tid; j < topk; j += kTopkThreads) {
+        if constexpr (MODE == kSelPart) cp[j] = make_uint2(0u, 0xffffffffu);
+        else o[j] = -1;
+    }
+}
+
+// Row parts for the two-stage selection: enough parts for Q * parts to
+// cover the device (at most 8), and enough that a part holds at most
+// kIdxMaxSeq positions; a part must hold more than topk positions and the
+// candidates of all parts (parts * topk) fit one workgroup's 32768 keys.
+// Returns the part count (1: one workgroup per row) and the part length.
+static int indexer_parts(int Q, int max_seq, int topk, int cus, int* chunk_out) {
+    const int minp = (max_seq + kIdxMaxSeq - 1) / kIdxMaxSeq;
+    const int want = std::max(minp, std::min(8, (cus + Q - 1) / std::max(Q, 1)));
+    for (int p = want; p >= std::max(2, minp); p--) {
+        const int chunk = (max_seq + p - 1) / p;
+        const int ch = (chunk + kTopkThreads - 1) / kTopkThreads * kTopkThreads;
+        const int pe = (max_seq + ch - 1) / ch;
+        if (pe >= 2 && topk < ch && (long)pe * topk <= kIdxMaxSeq) {
+            *chunk_out = ch;
+            return pe;
+        }
+    }
+    *chunk_out = max_seq;
+    return minp == 1 ? 1 : -1;
 }
 
 // compute units of the current device (256 on MI355X), looked up once per device
@@ -369,16 +436,30 @@ static int scores_blocks_per_cu() {
     return b;
 }
 
+size_t dsa_indexer_scratch_bytes(int Q, int max_seq, int topk) {
+    if (Q <= 0 || max_seq < 1 || max_seq > kIdxMaxRow || topk < 1) return 0;
+    int chunk = 0;
+    const int parts = indexer_parts(Q, max_seq, topk, device_cu_count(), &chunk);
+    return parts >= 2 ? (size_t)Q * parts * topk * sizeof(uint2) : 0;
+}
+
 int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
                        long kc_rows, const float* ks, const int* page_table, const int* seq_len,
                        int Q, int Hi, int page, int pages_per_seq, int max_seq, int topk,
-                       float* scores, int* out, hipStream_t st) {
+                       float* scores, int* out, void* scratch, size_t scratch_bytes, hipStream_t st) {
     AMDMOE_CHECK_ARG(Hi >= 16 && Hi <= kIdxMaxHeads && Hi % 16 == 0,
                      "dsa_indexer: Hi=%d must be a multiple of 16 in [16, %d]", Hi, kIdxMaxHeads);
-    AMDMOE_CHECK_ARG(max_seq >= 1 && max_seq <= kIdxMaxSeq, "dsa_indexer: max_seq=%d outside [1, %d]",
-                     max_seq, kIdxMaxSeq);
+    AMDMOE_CHECK_ARG(max_seq >= 1 && max_seq <= kIdxMaxRow, "dsa_indexer: max_seq=%d outside [1, %d]",
+                     max_seq, kIdxMaxRow);
     AMDMOE_CHECK_ARG(topk >= 1 && page >= 1 && pages_per_seq >= 1 && kc_rows >= 1,
                      "dsa_indexer: bad topk / paging");
+    int chunk = 0;
+    const int parts = indexer_parts(std::max(Q, 1), max_seq, topk, device_cu_count(), &chunk);
+    AMDMOE_CHECK_ARG(parts >= 1, "dsa_indexer: max_seq=%d above %d needs topk * parts <= %d (topk=%d)",
+                     max_seq, kIdxMaxSeq, kIdxMaxSeq, topk);
+    const size_t need = parts >= 2 ? (size_t)Q * parts * topk * sizeof(uint2) : 0;
+    AMDMOE_CHECK_ARG(scratch_bytes >= need && (need == 0 || scratch != nullptr),
+                     "dsa_indexer: scratch of %zu bytes, %zu needed", scratch_bytes, need);
     AMDMOE_CHECK_ARG(kc_rows * kIdxD < 0x7FFFFFF0L, "dsa_indexer: key cache of %ld rows exceeds 2 GiB", kc_rows);
     if (Q == 0) return AMDMOE_OK;
     const int ntile = (max_seq + kIdxTile - 1) / kIdxTile;
@@ -411,20 +492,33 @@ int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, cons
 #undef AMDMOE_IDX_LAUNCH
 #undef AMDMOE_IDX_LAUNCH2
     AMDMOE_LAUNCH_CHECK();
-    // registers hold ceil(max_seq / 1024) keys per thread, rounded up to a power of two
-    const int per = (max_seq + kTopkThreads - 1) / kTopkThreads;
+    // registers hold the keys of one selection, rounded up to a power of two per thread
     const int cap = (int)std::min<long>(max_seq, (long)pages_per_seq * page);
-#define AMDMOE_TOPK_LAUNCH(P)                                                                     \
-    hipLaunchKernelGGL(indexer_topk_kernel<P>, dim3((unsigned)Q), dim3(kTopkThreads), 0, st, scores, \
-                       seq_len, max_seq, cap, topk, out)
-    if (per <= 1) AMDMOE_TOPK_LAUNCH(1);
-    else if (per <= 2) AMDMOE_TOPK_LAUNCH(2);
-    else if (per <= 4) AMDMOE_TOPK_LAUNCH(4);
-    else if (per <= 8) AMDMOE_TOPK_LAUNCH(8);
-    else if (per <= 16) AMDMOE_TOPK_LAUNCH(16);
-    else AMDMOE_TOPK_LAUNCH(32);
+    uint2* cand = (uint2*)scratch;
+#define AMDMOE_TOPK_LAUNCH(P, MODE, GRID)                                                              \
+    hipLaunchKernelGGL((indexer_topk_kernel<P, MODE>), dim3((unsigned)(GRID)), dim3(kTopkThreads), 0, st, \
+                       scores, seq_len, max_seq, cap, topk, parts, chunk, cand, out)
+#define AMDMOE_TOPK_DISPATCH(KEYS, MODE, GRID)                   \
+    do {                                                         \
+        const int per = ((KEYS) + kTopkThreads - 1) / kTopkThreads; \
+        if (per <= 1) AMDMOE_TOPK_LAUNCH(1, MODE, GRID);         \
+        else if (per <= 2) AMDMOE_TOPK_LAUNCH(2, MODE, GRID);    \
+        else if (per <= 4) AMDMOE_TOPK_LAUNCH(4, MODE, GRID);    \
+        else if (per <= 8) AMDMOE_TOPK_LAUNCH(8, MODE, GRID);    \
+        else if (per <= 16) AMDMOE_TOPK_LAUNCH(16, MODE, GRID);  \
+        else AMDMOE_TOPK_LAUNCH(32, MODE, GRID);                 \
+        AMDMOE_LAUNCH_CHECK();                                   \
+    } while (0)
+    if (parts == 1) {
+        AMDMOE_TOPK_DISPATCH(max_seq, kSelFull, Q);
+    } else {
+        // each part's top-k (Q * parts workgroups), then the top-k of the
+        // parts' candidates
+        AMDMOE_TOPK_DISPATCH(chunk, kSelPart, (long)Q * parts);
+        AMDMOE_TOPK_DISPATCH(parts * topk, kSelMerge, Q);
+    }
+#undef AMDMOE_TOPK_DISPATCH
 #undef AMDMOE_TOPK_LAUNCH
-    AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
 

@@ -145,10 +145,11 @@ int launch_dsa_f32(const float* qn, const float* qp, const float* kc, const floa
 size_t dsa_paged_scratch_bytes(int Q, int H, int S);
 // dsa_indexer.hip: lightning-indexer scores [Q, max_seq] (scratch) and the
 // topk positions per query
+size_t dsa_indexer_scratch_bytes(int Q, int max_seq, int topk);
 int launch_dsa_indexer(const uint8_t* qc, const float* qs, const float* hw, const uint8_t* kc,
                        long kc_rows, const float* ks, const int* page_table, const int* seq_len,
                        int Q, int Hi, int page, int pages_per_seq, int max_seq, int topk,
-                       float* scores, int* out, hipStream_t st);
+                       float* scores, int* out, void* scratch, size_t scratch_bytes, hipStream_t st);
 int launch_dsa_bf16_paged(const uint16_t* qn, const uint16_t* qp, const uint16_t* cache,
                           long cache_tokens, const int* page_table, const int* logical,
                           uint16_t* out, int Q, int H, int Dc, int Dp, int S, int page,

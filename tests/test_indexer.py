@@ -103,6 +103,45 @@ def test_gpu_indexer_bit_exact_on_exact_scores(amd, orc, Q, Hi, ctx, page, topk)
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("Q,Hi,ctx,page,topk", [(2, 16, 100000, 64, 2048), (1, 16, 131072, 128, 4096),
+                                                (64, 16, 4096, 64, 512)])
+def test_gpu_indexer_long_rows_and_many_queries(amd, orc, Q, Hi, ctx, page, topk):
+    """Rows beyond one selection workgroup's 32768 keys (100000 and 131072
+    positions: 9 and 8 parts, each part's top-k then the top-k of the
+    candidates) and 64 queries (4 parts each), bit-exact against the oracle
+    on tie-rich exact scores."""
+    import torch
+    print(f"indexer parts Q={Q} Hi={Hi} ctx={ctx} topk={topk}", flush=True)
+    qc, qs, hw, kc, ks, pt = exact_inputs(Q, Hi, ctx, page, ctx + Q)
+    sl = np.array([ctx - 1001 * q for q in range(Q)], np.int32)
+    ref_sc = orc.dsa_indexer_scores(qc, qs, hw, kc, ks, pt, sl, page, ctx)
+    ref_ix = orc.dsa_indexer_topk(ref_sc, sl, topk)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    scores = torch.empty((Q, ctx), dtype=torch.float32, device="cuda")
+    out = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    amd.dsa_indexer_topk_fp8(d(qc), d(qs), d(hw), d(kc), d(ks), d(pt), d(sl), page, ctx, topk,
+                             scores, out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(scores.cpu().numpy(), ref_sc)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref_ix)
+
+
+@pytest.mark.gpu
+def test_gpu_indexer_rejects_unsplittable_long_row(amd):
+    """A row above 32768 positions whose parts' candidates would not fit one
+    workgroup (2 parts x topk 20000 > 32768) is refused, nothing launched."""
+    import torch
+    Q, Hi, ctx, page, topk = 1, 16, 40000, 64, 20000
+    qc, qs, hw, kc, ks, pt = exact_inputs(Q, Hi, ctx, page, 5)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    scores = torch.empty((Q, ctx), dtype=torch.float32, device="cuda")
+    out = torch.empty((Q, topk), dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="max_seq"):
+        amd.dsa_indexer_topk_fp8(d(qc), d(qs), d(hw), d(kc), d(ks), d(pt), d(np.array([ctx], np.int32)),
+                                 page, ctx, topk, scores, out)
+
+
+@pytest.mark.gpu
 def test_gpu_indexer_empty_and_overlong_sequences(amd, orc):
     """seq_len 0 (every score -inf, every index -1), seq_len past max_seq
     (clamped to max_seq) and seq_len 1, bit-exact against the oracle."""
