@@ -289,7 +289,11 @@ constexpr int kRtStage = (kRtTok + kRtExp) * 128;  // 40960
 constexpr int kRtNS = 3;
 constexpr int kRtLds = kRtNS * kRtStage;           // 122880
 constexpr int kRtMinBlocks = 256;                  // one per CU
-constexpr int kRtMaxSplit = 16;                    // partials summed per logit
+constexpr int kRtMaxSplit = 16;                    // partials summed per logit (one wave per token)
+// Decode-sized batches (one 64-token tile) split the gate into up to 64
+// chunks of one 128-column block each, so 56 workgroups share the gate's
+// 3.7 MB at DeepSeek-V3's shape; route_topk_block_kernel then sums them.
+constexpr int kRtMaxSplitSmall = 64;
 
 // K-steps (64 columns) per chunk and number of chunks.  With quantisation
 // a chunk is a whole number of 128-column blocks.
@@ -301,7 +305,8 @@ static RouteSplit route_split(int T, int D, bool quant) {
     const int units = nk / unit;
     const int tiles = (T + kRtTok - 1) / kRtTok;
     int want = (kRtMinBlocks + tiles - 1) / tiles;
-    want = want > kRtMaxSplit ? kRtMaxSplit : want;
+    const int cap = tiles == 1 ? kRtMaxSplitSmall : kRtMaxSplit;
+    want = want > cap ? cap : want;
     want = want < 1 ? 1 : (want > units ? units : want);
     const int kc = ((units + want - 1) / want) * unit;
     return {kc, (nk + kc - 1) / kc};
@@ -476,6 +481,35 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     wave_route_token_reg<KMAX>(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
+// route_topk_block_kernel: one 256-thread workgroup per token for gates
+// split into more than kRtMaxSplit chunks.  Thread e sums expert e's chunk
+// partials in chunk order (every chunk's load in flight at once, each load
+// instruction 1 KB contiguous across the workgroup), the logits go through
+// LDS, and wave 0 routes the token (wave_route_token_reg).
+template <int KMAX>
+__global__ __launch_bounds__(256) void route_topk_block_kernel(const float* __restrict__ part, int nsplit,
+                                                               int T, int E, int K, int* __restrict__ idx,
+                                                               float* __restrict__ wts) {
+    __shared__ float s_logit[256];
+    const int t = blockIdx.x, e = threadIdx.x;
+    float pv[kRtMaxSplitSmall];
+#pragma unroll
+    for (int i = 0; i < kRtMaxSplitSmall; i++)
+        pv[i] = i < nsplit && e < E ? part[((size_t)i * T + t) * E + e] : 0.0f;
+    float v = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRtMaxSplitSmall; i++)
+        if (i < nsplit) v = add_rn(v, pv[i]);
+    s_logit[e] = v;
+    __syncthreads();
+    if (threadIdx.x >= 64) return;  // wave 0 routes
+    const int lane = threadIdx.x;
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) r[j] = lane + 64 * j < E ? s_logit[lane + 64 * j] : -FLT_MAX;
+    wave_route_token_reg<KMAX>(r, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
+}
+
 // ---------------------------------------------------------------- launch
 template <typename XT, typename GT>
 int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int E, int K, int D,
@@ -514,7 +548,8 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
     const bool quant = xq != nullptr;
     AMDMOE_CHECK_ARG(!quant || (xs && D % 128 == 0), "routing: fused quantisation needs D %% 128 == 0");
     const RouteSplit sp = route_split(T, D, quant);
-    AMDMOE_CHECK_ARG(sp.nsplit >= 1 && sp.nsplit <= kRtMaxSplit, "routing: %d gate splits", sp.nsplit);
+    AMDMOE_CHECK_ARG(sp.nsplit >= 1 && sp.nsplit <= kRtMaxSplitSmall && (sp.nsplit <= kRtMaxSplit || T <= kRtTok),
+                     "routing: %d gate splits", sp.nsplit);
     {
         const int rc = ensure_dynamic_lds((const void*)route_logits_kernel, kRtLds);
         if (rc != AMDMOE_OK) return rc;
@@ -532,8 +567,20 @@ int launch_route_mfma(const uint16_t* x, const uint16_t* wg, int T, int E, int K
         case 8: topk = route_topk_kernel<8>; break;
         default: break;
     }
-    hipLaunchKernelGGL(topk, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, part, sp.nsplit, T, E,
-                       K, idx, wts);
+    if (sp.nsplit > kRtMaxSplit) {
+        auto topkb = route_topk_block_kernel<16>;
+        switch (route_kmax(K)) {
+            case 1: topkb = route_topk_block_kernel<1>; break;
+            case 2: topkb = route_topk_block_kernel<2>; break;
+            case 4: topkb = route_topk_block_kernel<4>; break;
+            case 8: topkb = route_topk_block_kernel<8>; break;
+            default: break;
+        }
+        hipLaunchKernelGGL(topkb, dim3((unsigned)T), dim3(256), 0, st, part, sp.nsplit, T, E, K, idx, wts);
+    } else {
+        hipLaunchKernelGGL(topk, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, part, sp.nsplit, T, E,
+                           K, idx, wts);
+    }
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
