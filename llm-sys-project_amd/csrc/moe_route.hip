@@ -1,5 +1,4 @@
-// R1 -- routing: gate logits, softmax over experts, top-K, renormalisation,
-// fused in one kernel per token block (the logits never leave the CU).
+// R1 -- routing: gate logits, softmax over experts, top-K, renormalisation.
 //
 // Reference semantics (kernels/moe/naive_moe.cu:87-142, the CPU copy in
 // tests/test_moe.cu:38-69):
@@ -15,8 +14,10 @@
 //     runs the reference's sequential fp32 sum (explicit round-to-nearest
 //     mul then add, never contracted), so logits are bit-identical to the
 //     reference's CPU loop.
-//   route_mfma_kernel  -- bf16 x and bf16 gate (DeepSeek-V3 shape, E=256,
-//     D=7168): the gate GEMM runs on bf16 MFMA with fp32 accumulation.
+//   route_logits_kernel -- bf16 x and bf16 gate (DeepSeek-V3 shape, E=256,
+//     D=7168): the gate GEMM runs on bf16 MFMA with fp32 accumulation, split
+//     along D over the CUs; route_topk_kernel / route_topk_block_kernel sum
+//     the chunk partials in chunk order.
 // Both then run the same wave routine: softmax with the reference's
 // sequential denominator, and a ballot-driven exact simulation of the
 // replace-min loop (only insertions cost work: ~K*(1+ln(E/K)) of them).
@@ -492,10 +493,14 @@ __global__ __launch_bounds__(256) void route_topk_block_kernel(const float* __re
                                                                float* __restrict__ wts) {
     __shared__ float s_logit[256];
     const int t = blockIdx.x, e = threadIdx.x;
+    // every load unconditional (chunks past nsplit re-read the last one and
+    // are not added; experts past E re-read expert E-1 and are not used):
+    // no per-load branch, no exec masks held across the batch
+    const int ec = min(e, E - 1);
     float pv[kRtMaxSplitSmall];
 #pragma unroll
     for (int i = 0; i < kRtMaxSplitSmall; i++)
-        pv[i] = i < nsplit && e < E ? part[((size_t)i * T + t) * E + e] : 0.0f;
+        pv[i] = part[((size_t)min(i, nsplit - 1) * T + t) * E + ec];
     float v = 0.0f;
 #pragma unroll
     for (int i = 0; i < kRtMaxSplitSmall; i++)
