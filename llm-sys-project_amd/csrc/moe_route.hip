@@ -94,14 +94,18 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
     // the experts of each 64-lane group that beat the current thr are taken
     // in ascending order from a ballot mask, which is re-formed after every
     // insertion from the new thr.
-    float sv = -FLT_MAX;
-    int si = -1;
-    float thr = -FLT_MAX;  // every slot starts at -FLT_MAX: the first victim is slot 0
-    int m = 0;
+    // Every slot starts at -FLT_MAX and every probability is >= 0, so the
+    // first min(K, E) experts are inserted in order into slots 0, 1, ...:
+    // that fill is one step, and the scan resumes at expert min(K, E).
+    const int k0 = min(K, E);  // uniform, <= 16: all in group 0
+    float sv = lane < k0 ? v[0] : -FLT_MAX;
+    int si = lane < k0 ? lane : -1;
+    float thr = slot_min<KMAX>(lane < K ? sv : INFINITY);
+    int m = __ffsll(__ballot(lane < K && sv == thr)) - 1;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         if (64 * j >= E) break;  // uniform
-        const bool valid = lane + 64 * j < E;
+        const bool valid = lane + 64 * j < E && (j > 0 || lane >= k0);
         unsigned long long cand = __ballot(valid && v[j] > thr);
         while (cand) {
             const int l = __ffsll(cand) - 1;  // next inserted expert: 64j + l
