@@ -78,9 +78,17 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
         if (64 * j >= E) break;  // uniform
         const int n = min(64, E - 64 * j);
         if (n == 64) {
+            // eight reads ahead of the adds that consume them
 #pragma unroll
-            for (int l = 0; l < 64; l++)
-                s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l)));
+            for (int b = 0; b < 64; b += 8) {
+                float r[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) r[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), b + i));
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) s = add_rn(s, r[i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         } else {
             for (int l = 0; l < n; l++) s = add_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l)));
         }
