@@ -328,6 +328,9 @@ def kernel_label(name):
         mode = ("UP", "DOWN")[int(m.group(2))]
         lay = "packed" if m.group(3) == "true" else "row-major"
         return f"grouped_gemm_kernel<{dt}, {mode}, {lay}>"
+    m = re.match(r"indexer_topk_kernel<(\d+), (\d)>", base)
+    if m:
+        return f"indexer_topk_kernel<{m.group(1)}, {('full', 'part', 'merge')[int(m.group(2))]}>"
     return base
 
 
