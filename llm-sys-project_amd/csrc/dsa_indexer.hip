@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
     constexpr int kWaves = kTopkThreads / 64;
     __shared__ __align__(16) int s_hist[kWaves][256];  // one histogram per wave
     __shared__ unsigned s_slice[kPer + 1];             // counts before each slice, total
-    __shared__ int s_sel[2];                           // digit, remaining count
+    __shared__ int s_sel[3];                           // digit, remaining count, keys with the digit
     __shared__ int s_nvalid;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qi = MODE == kSelPart ? blockIdx.x / nparts : blockIdx.x;
@@ -325,16 +325,20 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
                     const int cd = i == 0 ? c[0] : (i == 1 ? c[1] : (i == 2 ? c[2] : c[3]));
                     s_sel[0] = d;
                     s_sel[1] = need - (ge_d - cd);
+                    s_sel[2] = cd;
                 }
             }
             __syncthreads();
             prefix |= (uint32_t)s_sel[0] << shift;
             mask |= 0xffu << shift;
             need = s_sel[1];
+            // every key under the prefix is taken: the lower digits cannot
+            // change the selection (uniform: all threads read the same LDS)
+            if (need == s_sel[2]) break;
         }
     }
-    // prefix = the threshold key; slots above it are all taken, and the
-    // first `need` slots equal to it.  Slice j (slots j * 1024 + tid) is in
+    // prefix = the threshold key's leading bits under mask; slots above it
+    // are all taken, and the first `need` slots equal to it.  Slice j (slots j * 1024 + tid) is in
     // slot order across the workgroup, so each slot's output position is the
     // greater / equal keys of the slices before it, of the waves before it in
     // its slice (LDS counts) and of the lanes below it (ballots).
@@ -342,8 +346,8 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
         const bool valid = pos[j] >= 0;
-        const unsigned long long gm = __ballot(valid && (all || key[j] > prefix));
-        const unsigned long long em = __ballot(valid && !all && key[j] == prefix);
+        const unsigned long long gm = __ballot(valid && (all || (key[j] & mask) > prefix));
+        const unsigned long long em = __ballot(valid && !all && (key[j] & mask) == prefix);
         if (lane == 0) s_cnt[wave * kPer + j] = (unsigned)__popcll(gm) | ((unsigned)__popcll(em) << 16);
     }
     __syncthreads();
@@ -372,7 +376,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
         const bool valid = pos[j] >= 0;
-        const bool gt = valid && (all || key[j] > prefix), eq = valid && !all && key[j] == prefix;
+        const bool gt = valid && (all || (key[j] & mask) > prefix), eq = valid && !all && (key[j] & mask) == prefix;
         const unsigned long long gm = __ballot(gt), em = __ballot(eq);
         const unsigned base = s_slice[j] + s_cnt[wave * kPer + j];
         const int gb = (int)(base & 0xffff) + count_below(gm), eb = (int)(base >> 16) + count_below(em);
