@@ -84,6 +84,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypa
 // among the kept slots by expert id), and each thread loads all of its rows
 // (8 at a time, 4 column groups each) before adding them in that order, so
 // 32 loads per thread are in flight.
+template <int kG>  // 8-column groups per thread; blockIdx.y picks the block's 256 * kG groups
 __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __restrict__ ypair,
                                                            const int* __restrict__ idx, int T,
                                                            int K, int E, int D,
@@ -112,7 +113,8 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __res
     __syncthreads();
     const int n = s_n;
     const int ng = D / 8;  // 8-column groups
-    constexpr int kG = 4, kR = 8;
+    constexpr int kR = 8;
+    const int g0 = 256 * kG * blockIdx.y;  // this block's first column group
     f32x4 acc[kG][2];
 #pragma unroll
     for (int i = 0; i < kG; i++) acc[i][0] = acc[i][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __res
             const uint16_t* row = ypair + ((size_t)t * K + s_ord[jj < n ? jj : 0]) * D;
 #pragma unroll
             for (int i = 0; i < kG; i++) {
-                const int c = tid + 256 * i;
+                const int c = g0 + tid + 256 * i;
                 v[j][i] = (jj < n && c < ng) ? __builtin_nontemporal_load((const u32x4*)(row + 8 * c))
                                              : (u32x4){0u, 0u, 0u, 0u};
             }
@@ -143,7 +145,7 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __res
     }
 #pragma unroll
     for (int i = 0; i < kG; i++) {
-        const int c = tid + 256 * i;
+        const int c = g0 + tid + 256 * i;
         if (c >= ng) break;
         u32x4 o;
         for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(acc[i][m >> 1][2 * (m & 1)], acc[i][m >> 1][2 * (m & 1) + 1]);
@@ -158,8 +160,13 @@ int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int 
     if (dt == DT_F32)
         hipLaunchKernelGGL((combine_kernel<float, false>), dim3(T), dim3(256), 0, st,
                            (const float*)ypair, idx, T, K, E, D, y);
+    else if (D <= 8 * 256 * 4 && T <= 64)
+        // few tokens: a token's columns over several workgroups (one 8-column
+        // group per thread), so no CU streams a whole token's K rows alone
+        hipLaunchKernelGGL(combine_bf16_kernel<1>, dim3(T, (unsigned)ceil_div(D / 8, 256)), dim3(256), 0, st,
+                           (const uint16_t*)ypair, idx, T, K, E, D, (uint16_t*)y);
     else if (D <= 8 * 256 * 4)
-        hipLaunchKernelGGL(combine_bf16_kernel, dim3(T), dim3(256), 0, st, (const uint16_t*)ypair,
+        hipLaunchKernelGGL(combine_bf16_kernel<4>, dim3(T), dim3(256), 0, st, (const uint16_t*)ypair,
                            idx, T, K, E, D, (uint16_t*)y);
     else
         hipLaunchKernelGGL((combine_kernel<uint16_t, true>), dim3(T), dim3(256), 0, st,
