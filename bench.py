@@ -119,32 +119,85 @@ def cpu_single_core(K, D, I, n_tokens=16):
                       f"{dt:.1f} s; T=4096 extrapolated linearly"}
 
 
-def dsa_bench(amdmoe, synth, iters=20):
-    """BASELINE DSA decode: B=64, H=128, Dc=512, Dp=64, S=2048 of 32768."""
+def dsa_bench(amdmoe, synth, iters=20, cpu=False):
+    """BASELINE DSA decode: B=64, H=128, Dc=512, Dp=64, S=2048 of 32768.
+
+    Calls rotate over four decode batches (queries and selected positions)
+    over one 2.42 GB cache: each batch reads 151 MB of KV rows, the four
+    together ~580 MB of distinct rows, more than twice the 256 MB MALL, so a
+    timed call cannot find its rows cached by the call before."""
     import torch
     Q, H, S, page, ctx = 64, 128, 2048, 64, 32768
-    sets = [synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=s) for s in (5, 6)]
+    qn, qp, cache, pt, lg, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=5)
+    sets = [(qn, qp, lg)] + [synth.dsa_queries(Q, H, 512, 64, S, ctx, seed=s) for s in (6, 7, 8)]
     cfg = amdmoe.dsa_config(Q, H, 512, 64, S, page, Q * ctx)
     out = torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")
-    for st in sets:
-        qn, qp, cache, pt, lg, pps = st
-        amdmoe.dsa_decode_bf16_paged(qn, qp, cache, pt, lg, out, cfg, pps)
+    for a_, b_, c_ in sets:
+        amdmoe.dsa_decode_bf16_paged(a_, b_, cache, pt, c_, out, cfg, pps)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for i in range(iters):   # alternate two index sets: 302 MB > the 256 MB MALL
-        qn, qp, cache, pt, lg, pps = sets[i & 1]
-        amdmoe.dsa_decode_bf16_paged(qn, qp, cache, pt, lg, out, cfg, pps)
+    for i in range(iters):
+        a_, b_, c_ = sets[i % len(sets)]
+        amdmoe.dsa_decode_bf16_paged(a_, b_, cache, pt, c_, out, cfg, pps)
     b.record()
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1e3 / iters
     nbytes = Q * (S * 1152 + H * 576 * 2 + H * 512 * 2 + S * 4 + (ctx // page) * 4)
     flops = Q * H * S * (2 * 576 + 2 * 512)
-    del sets
-    return {"us_per_call": round(us, 2), "queries_per_s": round(Q / (us * 1e-6), 1),
-            "hbm_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4),
-            "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4)}
+    res = {"us_per_call": round(us, 2), "queries_per_s": round(Q / (us * 1e-6), 1),
+           "hbm_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4),
+           "bf16_mfma_frac": round(flops / (us * 1e-6) / 2.5e15, 4),
+           "rotation": f"{len(sets)} batches over one cache"}
+    if cpu:
+        res["cpu_baseline"] = dsa_cpu_baseline(qn, qp, cache, pt, lg, page)
+    del sets, cache
+    torch.cuda.empty_cache()
+    return res
+
+
+def dsa_cpu_baseline(qn, qp, cache, pt, lg, page, n_single=8):
+    """The oracle's restatement of the reference's cpu_dsa_forward
+    (tests/test_dsa.cu:23-68: per query gather of the selected rows, then per
+    head sequential fp32 dots, softmax and output sums) on the same decode
+    batch, its bf16 values decoded to fp32 and the selected rows gathered
+    through the page table beforehand (not timed): all 64 queries on every
+    host thread, and n_single queries on one core."""
+    import numpy as np
+    import torch
+
+    import oracle
+    Q, H, _ = qn.shape
+    S = lg.shape[1]
+    phys = oracle.dsa_translate(lg.cpu().numpy(), pt.cpu().numpy(), page)
+    rows = cache.index_select(0, torch.from_numpy(phys.reshape(-1).astype(np.int64)).cuda())
+    rows = oracle.bf16_to_f32(rows.cpu().numpy().view(np.uint16))          # [Q*S, 576]
+    kc, kp = rows[:, :512].copy(), rows[:, 512:].copy()
+    qnf = oracle.bf16_to_f32(qn.cpu().numpy().view(np.uint16))
+    qpf = oracle.bf16_to_f32(qp.cpu().numpy().view(np.uint16))
+    flat = np.arange(Q * S, dtype=np.int32).reshape(Q, S)
+    oracle.lib()
+    threads = oracle.get_threads()
+    t0 = time.perf_counter()
+    oracle.dsa_forward_f32(qnf, qpf, kc, kp, kc, flat)
+    dt = time.perf_counter() - t0
+    prev = oracle.get_threads()
+    oracle.set_threads(1)
+    try:
+        n = min(n_single, Q)
+        t0 = time.perf_counter()
+        oracle.dsa_forward_f32(qnf[:n], qpf[:n], kc, kp, kc, flat[:n])
+        dt1 = time.perf_counter() - t0
+    finally:
+        oracle.set_threads(prev)
+    return {"value": round(Q / dt, 2), "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"all {Q} queries of one BASELINE decode batch (H={H}, S={S}, Dc=512, Dp=64), "
+                      f"restatement of cpu_dsa_forward over OpenMP threads; {dt:.1f} s",
+            "cpu_model": cpu_model(),
+            "single_core": {"value": round(n / dt1, 3), "unit": "queries/s", "cores": 1, "kind": "port",
+                            "sample": f"{n} queries on one core (the reference's single-threaded "
+                                      f"loop); {dt1:.1f} s"}}
 
 
 def indexer_bench(amdmoe, synth, iters=20):
@@ -648,7 +701,7 @@ def main():
         result["mxfp4_layer"] = mxfp4_bench(amdmoe, synth)
     if not args.skip_dsa:
         log("[bench] DSA decode")
-        result["dsa_decode"] = dsa_bench(amdmoe, synth)
+        result["dsa_decode"] = dsa_bench(amdmoe, synth, cpu=args.cpu_sample > 0)
         log("[bench] DSA indexer")
         result["dsa_indexer"] = indexer_bench(amdmoe, synth)
     if args.cpu_sample > 0:

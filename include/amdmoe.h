@@ -174,7 +174,11 @@ int amdmoe_quant_rows_mxfp8(const uint16_t* x, long rows, int cols, uint8_t* q, 
 int amdmoe_pack_weights_mxfp4(const uint8_t* q, const uint8_t* scale, int num_experts, int rows,
                               int cols, uint8_t* q_packed, uint8_t* scale_packed, void* stream);
 
-/* Bytes of device scratch amdmoe_moe_forward_fp8_packed_noalloc owns per GPU. */
+/* Bytes of device scratch amdmoe_moe_forward_fp8_packed_noalloc owns per GPU.
+ * The array is a static device variable of the library's code object, so it
+ * is reserved on every GPU the library is loaded on, when the code object
+ * loads there, whether or not the entry is ever called (512 MiB on a host
+ * of 8 GPUs), and it is held until the process ends. */
 #define AMDMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* amdmoe_moe_forward_fp8_packed for callers that cannot allocate (code under
@@ -185,7 +189,7 @@ int amdmoe_pack_weights_mxfp4(const uint8_t* q, const uint8_t* scale, int num_ex
  * library, one per GPU, held until the process ends; the call allocates and
  * frees nothing.  Configurations whose workspace (amdmoe_moe_workspace_bytes
  * with AMDMOE_DTYPE_FP8) exceeds it are rejected with AMDMOE_ERR_WORKSPACE
- * (at the DeepSeek-V3 shape, T up to about 400 tokens fit).  Every call on
+ * (at the DeepSeek-V3 shape, E=256, K=8, D=7168, I=2048: T <= 432).  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (two
  * streams, two host threads) race and must be ordered by the caller. */
 int amdmoe_moe_forward_fp8_packed_noalloc(const uint16_t* x, const uint16_t* gate_weight,

@@ -9,8 +9,11 @@
 // Differences a caller can observe:
 //   - moe_forward does not block the host (the reference synchronises once
 //     per expert, naive_moe.cu:427-429); synchronise before reading `output`.
-//   - moe_forward needs D and I to be multiples of 32 (every shape in the
-//     reference's tests and benchmarks is).
+//   - none in the shapes accepted: moe_forward takes any D and I (multiples
+//     of 32 run the MFMA grouped GEMM, others a bounds-checked fp32 GEMM);
+//     shapes the reference mishandles (D > 1024 in its scatter launch,
+//     element counts past 2^31) work here, and K > 64 is rejected with an
+//     error instead.
 #pragma once
 
 #include <hip/hip_runtime.h>

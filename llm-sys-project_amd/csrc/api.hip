@@ -91,9 +91,10 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
         w.ypair = take(2 * P * D);
         w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E, (int)D, dtype == AMDMOE_DTYPE_FP8));
     } else {
-        const size_t es = elem_size(dtype);
-        w.act = take(es * P * I);
-        w.ypair = take(es * P * D);
+        // the down-projection's weighted rows stay fp32 on the fp32 and bf16
+        // paths, so a bf16 output is rounded once (in the combine)
+        w.act = take(elem_size(dtype) * P * I);
+        w.ypair = take(4 * P * D);
     }
     w.total = off;
     return w;
@@ -262,7 +263,8 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.sorted_w = w.sorted_w;
     TRY(launch_grouped_gemm(dt, MODE_DOWN, dn, mtiles, st));
     TRY(mark(5, st));
-    TRY(launch_combine(dt == DT_F32 ? DT_F32 : DT_BF16, w.ypair, w.idx, T, K, E, D, y, st));
+    TRY(launch_combine(dt == DT_F32 || dt == DT_BF16 ? DT_F32 : DT_BF16, dt == DT_F32 ? DT_F32 : DT_BF16,
+                       w.ypair, w.idx, T, K, E, D, y, st));
     return mark(6, st);
 }
 

@@ -123,9 +123,9 @@ int launch_pack_mxfp4(const uint8_t* q, const uint8_t* s, long E, int N, int K, 
 // K % 128 == 0)
 int launch_pack_weights(const uint8_t* w, long E, long N, long K, uint8_t* out, hipStream_t st);
 
-// moe_combine.hip
-int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,
-                   hipStream_t st);
+// moe_combine.hip: ypair rows fp32 or bf16 (DT_F32 / DT_BF16), y fp32 or bf16
+int launch_combine(int ypair_dt, int out_dt, const void* ypair, const int* idx, int T, int K, int E,
+                   int D, void* y, hipStream_t st);
 int launch_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
                           hipStream_t st);
 int launch_swiglu_f32(const float* gate, const float* up, float* out, int n, hipStream_t st);

@@ -153,12 +153,17 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __res
     }
 }
 
-int launch_combine(int dt, const void* ypair, const int* idx, int T, int K, int E, int D, void* y,
-                   hipStream_t st) {
+int launch_combine(int ypair_dt, int out_dt, const void* ypair, const int* idx, int T, int K, int E,
+                   int D, void* y, hipStream_t st) {
     AMDMOE_CHECK_ARG(K <= 64 && D % 8 == 0, "combine: K=%d D=%d unsupported", K, D);
+    AMDMOE_CHECK_ARG(ypair_dt == DT_F32 || out_dt == DT_BF16, "combine: bf16 rows need a bf16 output");
     if (T == 0) return AMDMOE_OK;
-    if (dt == DT_F32)
+    if (ypair_dt == DT_F32 && out_dt == DT_F32)
         hipLaunchKernelGGL((combine_kernel<float, false>), dim3(T), dim3(256), 0, st,
+                           (const float*)ypair, idx, T, K, E, D, y);
+    else if (ypair_dt == DT_F32)
+        // fp32 rows, bf16 output (the bf16 layer): the sum is rounded once
+        hipLaunchKernelGGL((combine_kernel<float, true>), dim3(T), dim3(256), 0, st,
                            (const float*)ypair, idx, T, K, E, D, y);
     else if (D <= 8 * 256 * 4 && T <= 64)
         // few tokens: a token's columns over several workgroups (one 8-column

@@ -857,8 +857,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // LDS (staged in the prologue)
         const int* s_slot = (const int*)(smem + kRowInfoOff);
         const float* s_wt = (const float*)(smem + kRowInfoOff) + kBM;
-        if (DT == DT_F32) {
-            // fp32 (the reference path): 16-byte stores straight from the accumulators
+        if (DT == DT_F32 || DT == DT_BF16) {
+            // fp32 rows (the reference path, and the bf16 layer, whose output
+            // is then rounded once, in the combine): 16-byte stores straight
+            // from the accumulators
 #pragma unroll
             for (int rt = 0; rt < 16; rt++) {
                 if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
@@ -874,7 +876,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 }
             }
         } else {
-            // bf16: the weighted rows are staged through the (now idle) ring,
+            // fp8 / MX (bf16 rows): the weighted rows are staged through the (now idle) ring,
             // 128 rows per pass as bf16, then every thread stores 16
             // contiguous bytes: one instruction writes two full 512-byte row
             // segments instead of 16 rows x 32 bytes.

@@ -102,10 +102,14 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
     // the experts of each 64-lane group that beat the current thr are taken
     // in ascending order from a ballot mask, which is re-formed after every
     // insertion from the new thr.
-    // Every slot starts at -FLT_MAX and every probability is >= 0, so the
-    // first min(K, E) experts are inserted in order into slots 0, 1, ...:
-    // that fill is one step, and the scan resumes at expert min(K, E).
-    const int k0 = min(K, E);  // uniform, <= 16: all in group 0
+    // Every slot starts at -FLT_MAX, so when the first min(K, E) experts all
+    // beat it (finite probabilities are >= 0) they are inserted in order into
+    // slots 0, 1, ...: that fill is one step, and the scan resumes at expert
+    // min(K, E).  A non-finite logit makes every probability NaN, which
+    // beats nothing: then the scan runs from expert 0 and, as in the
+    // reference, inserts nothing (indices -1, weights -FLT_MAX).
+    int k0 = min(K, E);  // uniform, <= 16: all in group 0
+    if (__ballot(lane < k0 && !(v[0] > -FLT_MAX))) k0 = 0;
     float sv = lane < k0 ? v[0] : -FLT_MAX;
     int si = lane < k0 ? lane : -1;
     float thr = slot_min<KMAX>(lane < K ? sv : INFINITY);

@@ -107,6 +107,16 @@ def dsa_paged(Q, H, Dc, Dp, S, page, ctx, seed=5, device="cuda"):
     return (qn.view(torch.int16), qp.view(torch.int16), cache.view(torch.int16), pt, logical, pps)
 
 
+def dsa_queries(Q, H, Dc, Dp, S, ctx, seed, device="cuda"):
+    """Another decode batch over an existing cache (dsa_paged's layout):
+    bf16 q_nope / q_pe ~ N(0,1) and S distinct logical positions per query."""
+    g = _gen(seed, device)
+    logical = torch.stack([torch.randperm(ctx, generator=g, device=device)[:S] for _ in range(Q)])
+    qn = torch.randn((Q, H, Dc), generator=g, device=device).to(torch.bfloat16)
+    qp = torch.randn((Q, H, Dp), generator=g, device=device).to(torch.bfloat16)
+    return qn.view(torch.int16), qp.view(torch.int16), logical.to(torch.int32).contiguous()
+
+
 def dsa_indexer(Q, Hi, ctx, page, seed=9, page_table=None, device="cuda"):
     """Lightning-indexer inputs: fp8 e4m3 query heads [Q,Hi,128] and keys
     [Q*ctx,128] (paged like the latent cache), each row quantised with one

@@ -77,9 +77,10 @@ def test_dsa_bf16_paged_ragged_s(amd, orc):
 
 
 def test_dsa_bf16_paged_baseline_shape(amd, orc):
-    """B=64, H=128, S=2048 of 32768-token contexts; 4 queries checked."""
+    """B=64, H=128, S=2048 of 32768-token contexts; 16 of the 64 queries
+    checked (every fourth, so both ends and every XCD's share of the grid)."""
     print("dsa_bf16 baseline", flush=True)
-    assert _paged_case(amd, orc, 64, 128, 2048, 32768, check_q=[0, 17, 42, 63]) < 1e-2
+    assert _paged_case(amd, orc, 64, 128, 2048, 32768, check_q=list(range(0, 64, 4)) + [63]) < 1e-2
 
 
 # H a multiple of 128: the token-split kernel (workgroup = query x 128 heads

@@ -2,10 +2,11 @@
 
 Bars: integer outputs (expert indices, permutation, fp8 codes) bit-exact;
 fp32 outputs within the reference's max-abs tolerances
-(tests/test_moe.cu:204-267, strict <); bf16 outputs within 1e-2 max-abs of
-the oracle's fp32 result, or within one bf16 step where |y| >= 2 (a step
-there, 0.0156, exceeds 1e-2; bf16_bar_ok); fp8 outputs within 2e-2 relative (max-abs error
-over max |ref|) of the oracle run on the same dequantised fp8 values.
+(tests/test_moe.cu:204-267, strict <); bf16 outputs within the reference's
+1e-2 max-abs of the oracle's fp32 result, widened only where the output's own
+rounding (half a bf16 step) plus a 1e-3 allowance exceeds it, i.e. |y| >= 4
+(bf16_bar_ok); fp8 outputs within 2e-2 relative (max-abs error over max
+|ref|) of the oracle run on the same dequantised fp8 values.
 """
 import numpy as np
 import pytest
@@ -201,11 +202,43 @@ def test_gate_bias_and_bf16x(amd, orc):
     np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6)
 
 
+@pytest.mark.parametrize("entry,T,E,K,D", [("f32", 64, 256, 8, 512), ("bf16", 1, 256, 8, 7168),
+                                           ("bf16", 64, 256, 8, 7168), ("bf16", 4096, 256, 8, 7168)])
+def test_gate_non_finite_token_selects_nothing(amd, orc, entry, T, E, K, D):
+    """A token with a NaN or inf in x has no finite logit: as in
+    tests/test_moe.cu:52-68 no expert is inserted (indices -1, weights
+    -FLT_MAX); every other token routes bit-exactly as the oracle's.  Covers
+    the fp32 gate and the bf16 MFMA gate's decode (T=1) and chunked top-k
+    kernels."""
+    announce(f"gate_{entry} non-finite token T={T}")
+    x, wg = _exact_gate_inputs(T, E, D, 21)
+    bad = [0] if T == 1 else [0, T // 2, T - 1]
+    x[bad[0], 3] = np.nan
+    if T > 1:
+        x[bad[1], D - 1] = np.inf
+        x[bad[2], 100] = -np.inf
+    idx_ref, wts_ref = orc.moe_route(x, wg, K)
+    assert (idx_ref[bad] == -1).all()
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    cfg = amd.moe_config(T, E, K, D, 128)
+    if entry == "f32":
+        amd.moe_gate_f32(dev(x), dev(wg), idx, wts, cfg)
+    else:
+        amd.moe_gate_bf16(dev(orc.f32_to_bf16(x)), dev(orc.f32_to_bf16(wg)), idx, wts, cfg)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_array_equal(host(wts)[bad], wts_ref[bad])
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6, atol=0)
+
+
 # ------------------------------------------------------------------ permutation
 # (70, 2048, 4): E > 1024 takes the single-launch kernel; the others the
 # three-launch one (incl. a partial last block of 64 tokens and K > E)
+# (8256, 256, 8): 129 token blocks, past 8192 tokens: the scan runs as its
+# own launch between the count and the scatter
 @pytest.mark.parametrize("T,E,K", [(1, 4, 2), (4, 16, 2), (512, 8, 2), (4096, 256, 8), (300, 3, 5),
-                                   (8192, 256, 8), (70, 2048, 4)])
+                                   (8192, 256, 8), (70, 2048, 4), (8256, 256, 8), (20000, 64, 6)])
 def test_permute_bit_exact(amd, orc, T, E, K):
     announce(f"permute T={T} E={E} K={K}")
     rng = np.random.default_rng(T + E)
@@ -347,10 +380,16 @@ def bf16_steps(got, ref):
 
 
 def bf16_bar_ok(got, ref):
-    """The reference's large-case bar (max-abs 1e-2, tests/test_moe.cu:204-267)
-    where a bf16 output can meet it, one bf16 step where that step exceeds
-    1e-2 (|y| >= 2: a step at [2, 4) is 0.0156, more than the bar itself)."""
-    bar = np.maximum(1e-2, np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -100))) - 7))
+    """The reference's large-case bar (max-abs 1e-2, tests/test_moe.cu:204-267),
+    or, where larger, half a bf16 step at |ref| (the output's own rounding:
+    the bf16 layer sums its per-expert rows in fp32 and rounds y once) plus
+    1e-3 for the rest: the intermediate activation is bf16 in both the GPU
+    path and the oracle, and the GPU's SwiGLU (hardware exp2 and reciprocal)
+    and fp32 summation order can flip an activation's last bit, each flip
+    moving y by ~1e-5 at these shapes.  The widening acts only where
+    |y| >= 4 (half a step there is 0.0156)."""
+    half = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -100))) - 8)
+    bar = np.maximum(1e-2, half + 1e-3)
     return bool((np.abs(got - ref) < bar).all())
 
 
@@ -374,15 +413,6 @@ def test_forward_bf16_multi_mtile_experts(amd, orc):
     announce("forward_bf16 multi-M-tile experts")
     err, y_ref, _ = _bf16_case(amd, orc, 1024, 4, 2, 128, 256, bias=True)
     assert err < 2.0 ** -7 * np.abs(y_ref).max()
-
-
-def test_forward_bf16_mixtral_t4096_sampled(amd, orc):
-    """T=4096 on the GPU; the oracle checks 24 tokens (each token's output
-    depends only on its own row)."""
-    announce("forward_bf16 mixtral T=4096 sampled")
-    rows = np.random.default_rng(3).choice(4096, 24, replace=False)
-    err, y_ref, yg = _bf16_case(amd, orc, 4096, 8, 2, 4096, 14336, bias=False, sample=rows)
-    assert bf16_bar_ok(yg, y_ref)
 
 
 # ------------------------------------------------------------------ forward fp8
@@ -690,20 +720,13 @@ def test_forward_every_tile_group_f32_bf16(amd, orc, dtype):
     assert err < bar
 
 
-def test_forward_fp8_dsv3_t4096_tile_edges(amd, orc, dsv3):
-    """T=4096 on the GPU; the oracle checks 256 tokens: every token that is
-    the first or the last sorted row of an M-tile (from the GPU's own routing
-    and permutation: tokens sort ascending within an expert, so these are
-    low and high token ids, ~180 of them), where a tile's row bounds and
-    masks act, and random others up to 256."""
-    import synth
-    T, E, K, D, I = 4096, 256, 8, 7168, 2048
-    announce("forward_fp8 dsv3 T=4096, 256 tile-edge tokens")
-    x, wg = synth.dsv3_inputs(T, E, D, seed=1235)
-    cfg = amd.moe_config(T, E, K, D, I)
-    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
-    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
-    amd.moe_gate_bf16(x, wg, idx, wts, cfg)
+def _tile_edge_sample(amd, idx, cfg, T, E, K, n_rows, seed):
+    """Tokens that are the first or the last sorted row of an M-tile, from the
+    GPU's own routing and permutation (tokens sort ascending within an
+    expert, so these are low and high token ids), where a tile's row bounds
+    and masks act; topped up with random tokens to n_rows.  Returns the rows
+    and the number of edge tokens among them (all of them when there are at
+    most n_rows)."""
     counts = torch.empty(E, dtype=torch.int32, device="cuda")
     offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
     st = torch.empty(T * K, dtype=torch.int32, device="cuda")
@@ -717,18 +740,59 @@ def test_forward_fp8_dsv3_t4096_tile_edges(amd, orc, dsv3):
         for rows in _mtile_rows(int(cn[e])):
             edges += [int(stn[first]), int(stn[first + rows - 1])]
             first += rows
-    rng = np.random.default_rng(4)
+    rng = np.random.default_rng(seed)
     edge_rows = np.unique(np.array(edges))
-    assert 100 <= len(edge_rows) <= 256
+    if len(edge_rows) > n_rows:
+        edge_rows = np.sort(rng.choice(edge_rows, n_rows, replace=False))
     rest = np.setdiff1d(np.arange(T), edge_rows)
-    rows = np.sort(np.concatenate([edge_rows, rng.choice(rest, 256 - len(edge_rows), replace=False)]))
-    assert len(rows) == 256
+    rows = np.sort(np.concatenate([edge_rows, rng.choice(rest, n_rows - len(edge_rows), replace=False)]))
+    assert len(rows) == n_rows
+    return rows, len(edge_rows)
+
+
+@pytest.mark.parametrize("T,n_rows", [(4096, 256), (8192, 640)])
+def test_forward_fp8_dsv3_tile_edges(amd, orc, dsv3, T, n_rows):
+    """DSV3 T=4096 and T=8192 on the GPU; the oracle checks every token that
+    is the first or last row of an M-tile (~180 at T=4096, where each expert
+    is one M-tile; several hundred at T=8192, where about half the experts
+    split into two) plus random others."""
+    import synth
+    E, K, D, I = 256, 8, 7168, 2048
+    announce(f"forward_fp8 dsv3 T={T}, {n_rows} tile-edge tokens")
+    x, wg = synth.dsv3_inputs(T, E, D, seed=1235)
+    cfg = amd.moe_config(T, E, K, D, I)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16(x, wg, idx, wts, cfg)
+    rows, n_edge = _tile_edge_sample(amd, idx, cfg, T, E, K, n_rows, seed=4)
+    print(f"edge tokens checked: {n_edge}")
+    assert n_edge >= 100
     assert _fp8_case(amd, orc, dsv3, T, E, K, D, I, sample=rows) < 2e-2
+
+
+def test_forward_bf16_mixtral_t4096_tile_edges(amd, orc):
+    """Mixtral bf16 T=4096 (every expert ~1024 rows, four M-tiles): the
+    oracle checks the first and last token of every M-tile plus random
+    others, 128 tokens."""
+    import synth
+    T, E, K, D, I = 4096, 8, 2, 4096, 14336
+    announce("forward_bf16 mixtral T=4096 tile edges")
+    x, wg, _, _, _ = synth.bf16_layer(T, E, D, I, seed=7, bias=False)
+    cfg = amd.moe_config(T, E, K, D, I)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    amd.moe_gate_bf16x(x, wg, None, idx, wts, cfg)
+    rows, n_edge = _tile_edge_sample(amd, idx, cfg, T, E, K, 128, seed=5)
+    del x, wg
+    print(f"edge tokens checked: {n_edge}")
+    assert n_edge >= 40
+    err, y_ref, yg = _bf16_case(amd, orc, T, E, K, D, I, bias=False, sample=rows, seed=7)
+    assert bf16_bar_ok(yg, y_ref)
 
 
 def test_forward_bf16_mixtral_t256(amd, orc):
     """BASELINE Mixtral config at T=256, every token checked (outputs reach
-    |y| ~ 2.6, where one bf16 step is 0.0156: the bar is bf16_bar_ok's)."""
+    |y| ~ 2.6, where bf16_bar_ok is the reference's 1e-2)."""
     announce("forward_bf16 mixtral T=256")
     err, y_ref, yg = _bf16_case(amd, orc, 256, 8, 2, 4096, 14336, bias=False)
     assert bf16_bar_ok(yg, y_ref)

@@ -191,6 +191,28 @@ def test_route_zero_input_and_duplicate_rows(orc):
     np.testing.assert_allclose(wts.sum(1), 1.0, rtol=1e-5)
 
 
+def test_route_non_finite_logits_select_nothing(orc):
+    """tests/test_moe.cu:38-68 with a NaN or inf in a token's logits: softmax
+    turns every probability of that token into NaN (max is inf, or the sum is
+    NaN), `v > slot` is false for NaN, so no expert is inserted: indices stay
+    -1 and weights -FLT_MAX (their sum is -inf, not > 0, so they are not
+    renormalised).  The other tokens route normally."""
+    T, E, K, D = 4, 8, 3, 64
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    wg = rng.standard_normal((E, D)).astype(np.float32)
+    idx0, wts0 = orc.moe_route(x, wg, K)
+    x[1, 5] = np.nan
+    x[2, 7] = np.inf
+    idx, wts = orc.moe_route(x, wg, K)
+    for t in (1, 2):
+        assert (idx[t] == -1).all()
+        assert (wts[t] == -np.finfo(np.float32).max).all()
+    for t in (0, 3):
+        np.testing.assert_array_equal(idx[t], idx0[t])
+        np.testing.assert_array_equal(wts[t], wts0[t])
+
+
 def test_route_bias_shifts_logits(orc):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((4, 64)).astype(np.float32)
