@@ -272,13 +272,20 @@ def _time_calls(fn, iters, warmup=3):
     return a.elapsed_time(b) / iters
 
 
-def sweep(amdmoe, synth, iters):
-    """Every MoE / DSA configuration of BASELINE.json, one row each.
+def sweep(amdmoe, synth, iters, only=None):
+    """Every MoE / DSA configuration of BASELINE.json, one row each (only
+    those whose row name matches the regular expression `only`, if given:
+    a profiler run can then cover one configuration alone).
 
     floor_ms = max(algorithmic HBM bytes / 8 TB/s, FLOPs / dense peak) --
     the roofline of the whole layer; attainable = floor_ms / ms."""
+    import re
+
     import torch
     rows = []
+
+    def want(name):
+        return only is None or re.search(only, name) is not None
 
     def row(name, dtype, T, E, K, D, I, ms, w_bytes, act_bytes, peak, active):
         flops = 6 * T * K * D * I
@@ -306,6 +313,8 @@ def sweep(amdmoe, synth, iters):
     # tiny and medium fp32 (reference signature: no gate bias), medium bf16 with bias
     for name, (T, E, K, D, I) in (("tiny_fp32", (4, 4, 2, 64, 128)),
                                   ("medium_fp32", (512, 8, 2, 1024, 2048))):
+        if not want(name):
+            continue
         g = torch.Generator(device="cuda")
         g.manual_seed(11)
         x = torch.randn((T, D), generator=g, device="cuda")
@@ -324,6 +333,8 @@ def sweep(amdmoe, synth, iters):
     bf16_cfgs += [(f"mixtral_bf16_T{T}", (T, 8, 2, 4096, 14336), False) for T in (16, 256, 4096)]
     layer = None
     for name, (T, E, K, D, I), bias in bf16_cfgs:
+        if not want(name):
+            continue
         if layer is None or layer[0] != (E, D, I, bias) or layer[1].shape[0] < T:
             layer = None
             torch.cuda.empty_cache()
@@ -343,12 +354,17 @@ def sweep(amdmoe, synth, iters):
     torch.cuda.empty_cache()
     # DeepSeek-V3 fp8 block-scale, packed (headline layout) and row-major
     E, K, D, I = 256, 8, 7168, 2048
+    fp8_tokens = [T for T in (1, 64, 512, 4096, 8192)
+                  if want(f"dsv3_fp8_T{T}_packed") or want(f"dsv3_fp8_T{T}_row-major")]
+    mx_tokens = tuple(T for T in (1, 64, 512, 4096, 8192) if want(f"dsv3_mxfp4_T{T}"))
+    if not fp8_tokens:
+        return _sweep_mx(amdmoe, synth, iters, mx_tokens, row, rows)
     w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=1234)
     w1p, w2p = torch.empty_like(w1q), torch.empty_like(w2q)
     amdmoe.pack_weights_fp8(w1q, w1p)
     amdmoe.pack_weights_fp8(w2q, w2p)
     xa, wg = synth.dsv3_inputs(8192, E, D, seed=99)
-    for T in (1, 64, 512, 4096, 8192):
+    for T in fp8_tokens:
         x = xa[:T].contiguous()
         y = torch.empty((T, D), dtype=torch.int16, device="cuda")
         cfg = amdmoe.moe_config(T, E, K, D, I)
@@ -357,13 +373,22 @@ def sweep(amdmoe, synth, iters):
         wb = act * (3 * I * D + ((2 * I // 128) * (D // 128) + (D // 128) * (I // 128)) * 4) + E * D * 2
         for lay, (a1, a2, fwd) in (("packed", (w1p, w2p, amdmoe.moe_forward_fp8_packed)),
                                    ("row-major", (w1q, w2q, amdmoe.moe_forward_fp8))):
+            if not want(f"dsv3_fp8_T{T}_{lay}"):
+                continue
             ms = _time_calls(lambda: fwd(x, wg, a1, w1s, a2, w2s, y, cfg, ws=ws), iters)
             row(f"dsv3_fp8_T{T}_{lay}", "fp8_e4m3", T, E, K, D, I, ms, wb, 2 * T * D * 2,
                 FP8_PEAK, act)
         del x, y, ws
     del w1q, w1s, w2q, w2s, w1p, w2p, xa, wg
     torch.cuda.empty_cache()
-    for name, r in mxfp4_bench(amdmoe, synth, iters, tokens=(1, 64, 512, 4096, 8192)).items():
+    return _sweep_mx(amdmoe, synth, iters, mx_tokens, row, rows)
+
+
+def _sweep_mx(amdmoe, synth, iters, tokens, row, rows):
+    """The MXFP4 rows of the sweep."""
+    if not tokens:
+        return rows
+    for name, r in mxfp4_bench(amdmoe, synth, iters, tokens=tokens).items():
         T = int(name[1:])
         row(f"dsv3_mxfp4_{name}", "mxfp4", T, 256, 8, 7168, 2048, r["ms"],
             r["experts_active"] * 3 * 2048 * 7168 * (0.5 + 1 / 32) + 256 * 7168 * 2, 2 * T * 7168 * 2,
@@ -546,6 +571,9 @@ def main():
     ap.add_argument("--sweep", metavar="JSON",
                     help="instead of the headline line, time every BASELINE MoE config and "
                          "write the rows to JSON")
+    ap.add_argument("--only", metavar="REGEX",
+                    help="with --sweep: only the rows whose config name matches (e.g. one "
+                         "configuration per profiler run)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
@@ -570,36 +598,40 @@ def main():
     import amdmoe
     import synth
     torch.cuda.set_device(0)
-    if args.sweep:
-        rows = sweep(amdmoe, synth, args.steps)
-        ix = indexer_bench(amdmoe, synth)
-        log(f"[sweep] dsa indexer: {ix}")
-        rows.append({"config": "dsa_decode_B64_H128_S2048", **dsa_bench(amdmoe, synth)})
-        log(f"[sweep] dsa: {rows[-1]}")
-        with open(args.sweep, "w") as f:
-            json.dump(rows, f, indent=1)
-        md = ["| config | ms | tokens/s | TFLOP/s | % dense peak | floor ms | % of floor |",
-              "|---|---:|---:|---:|---:|---:|---:|"]
-        for r in rows[:-1]:
-            md.append(f"| {r['config']} | {r['ms']:.4f} | {r['tokens_per_s']:.0f} | {r['tflops']:.1f} | "
-                      f"{100 * r['mfma_peak_frac']:.1f}% | {r['floor_ms']:.4f} | "
-                      f"{100 * r['attainable_frac']:.1f}% |")
-        d = rows[-1]
-        md.append(f"| {d['config']} (bf16, paged) | {d['us_per_call'] / 1e3:.4f} | "
-                  f"{d['queries_per_s']:.0f} queries/s | {100 * d['bf16_mfma_frac']:.1f}% of bf16 | | "
-                  f"{0.0212:.4f} | {100 * d['hbm_frac']:.1f}% of HBM peak |")
-        md.append(f"| dsa_indexer ({ix['shape']}, fp8) | {ix['us_per_call'] / 1e3:.4f} | "
-                  f"{ix['queries_per_s']:.0f} queries/s | {100 * ix['fp8_mfma_frac']:.1f}% of fp8 | | | "
-                  f"{100 * ix['hbm_frac']:.1f}% of HBM peak |")
-        with open(os.path.splitext(args.sweep)[0] + ".md", "w") as f:
-            f.write("\n".join(md) + "\n")
-        return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.sweep:
+        import re
+        rows = sweep(amdmoe, synth, args.steps, args.only)
+        md = ["| config | ms | tokens/s | TFLOP/s | % dense peak | floor ms | % of floor |",
+              "|---|---:|---:|---:|---:|---:|---:|"]
+        for r in rows:
+            md.append(f"| {r['config']} | {r['ms']:.4f} | {r['tokens_per_s']:.0f} | {r['tflops']:.1f} | "
+                      f"{100 * r['mfma_peak_frac']:.1f}% | {r['floor_ms']:.4f} | "
+                      f"{100 * r['attainable_frac']:.1f}% |")
+        if args.only is None or re.search(args.only, "dsa_decode_B64_H128_S2048"):
+            d = {"config": "dsa_decode_B64_H128_S2048", **dsa_bench(amdmoe, synth)}
+            log(f"[sweep] dsa: {d}")
+            rows.append(d)
+            md.append(f"| {d['config']} (bf16, paged) | {d['us_per_call'] / 1e3:.4f} | "
+                      f"{d['queries_per_s']:.0f} queries/s | {100 * d['bf16_mfma_frac']:.1f}% of bf16 | | "
+                      f"{0.0212:.4f} | {100 * d['hbm_frac']:.1f}% of HBM peak |")
+        if args.only is None or re.search(args.only, "dsa_indexer"):
+            ix = indexer_bench(amdmoe, synth)
+            log(f"[sweep] dsa indexer: {ix}")
+            rows.append({"config": "dsa_indexer", **ix})
+            md.append(f"| dsa_indexer ({ix['shape']}, fp8) | {ix['us_per_call'] / 1e3:.4f} | "
+                      f"{ix['queries_per_s']:.0f} queries/s | {100 * ix['fp8_mfma_frac']:.1f}% of fp8 | | | "
+                      f"{100 * ix['hbm_frac']:.1f}% of HBM peak |")
+        with open(args.sweep, "w") as f:
+            json.dump(rows, f, indent=1)
+        with open(os.path.splitext(args.sweep)[0] + ".md", "w") as f:
+            f.write("\n".join(md) + "\n")
+        return
     T, E, K, D, I = args.tokens, 256, 8, 7168, 2048
     log(f"[bench] generating DSV3 fp8 weights E={E} D={D} I={I}")
     w1q, w1s, w2q, w2s = synth.dsv3_weights(E, D, I, seed=1234)

@@ -18,9 +18,10 @@
 //     D=7168): the gate GEMM runs on bf16 MFMA with fp32 accumulation, split
 //     along D over the CUs; route_topk_kernel / route_topk_block_kernel sum
 //     the chunk partials in chunk order.
-// Both then run the same wave routine: softmax with the reference's
-// sequential denominator, and a ballot-driven exact simulation of the
-// replace-min loop (only insertions cost work: ~K*(1+ln(E/K)) of them).
+// Both then run the same wave routine: softmax (with the reference's
+// sequential denominator for the fp32 gate, a wave tree sum after the MFMA
+// gate), and a ballot-driven exact simulation of the replace-min loop (only
+// insertions cost work: ~K*(1+ln(E/K)) of them).
 #include "internal.hpp"
 
 #include <float.h>
@@ -62,7 +63,17 @@ __device__ __forceinline__ float slot_min(float v) {
 
 // Routing of one token by one wave, E <= 256, K <= KMAX <= 16: `v` holds
 // the logits of experts lane + 64j (j < 4; -FLT_MAX past E).
-template <int KMAX>
+// SEQ: the softmax denominator in the reference's order (ascending expert,
+// one add at a time), for logits that are bit-identical to the reference's
+// (the fp32 gate), so the weights are too.  Otherwise a tree sum over the
+// wave (every lane gets the same value): for the MFMA gates, whose logits
+// differ from the reference's sequential fp32 sums by rounding anyway.  The
+// denominator scales every probability alike, so the order of the
+// probabilities, and with it the selection, is the same either way
+// wherever distinct logits are farther apart than the rounding of one
+// division (always, for the exactly representable logits the parity tests
+// use); the weights move by at most a few ulps.
+template <int KMAX, bool SEQ = true>
 __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, float* out_wts) {
     const int lane = lane_id();
     // softmax (tests/test_moe.cu:14-20)
@@ -70,11 +81,12 @@ __device__ void wave_route_token_reg(float (&v)[4], int E, int K, int* out_idx, 
     mx = wave_max(mx);
 #pragma unroll
     for (int j = 0; j < 4; j++) v[j] = lane + 64 * j < E ? expf(v[j] - mx) : 0.0f;
-    // The denominator is summed in ascending expert order, exactly as the
-    // reference does: lane values are read out one by one (v_readlane).
+    // SEQ: the denominator is summed in ascending expert order, exactly as
+    // the reference does: lane values are read out one by one (v_readlane).
     float s = 0.0f;
+    if constexpr (!SEQ) s = wave_sum((v[0] + v[1]) + (v[2] + v[3]));  // 0 past E
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 4 && SEQ; j++) {
         if (64 * j >= E) break;  // uniform
         const int n = min(64, E - 64 * j);
         if (n == 64) {
@@ -227,9 +239,50 @@ __device__ __forceinline__ void load8_f(const uint16_t* p, float (&v)[8]) {
     }
 }
 
+// 32 consecutive elements of a row, as loaded (16-byte loads, row 16-byte
+// aligned); get<i>() converts element i to fp32.  Keeping the raw registers
+// lets many chunks' loads be in flight while earlier chunks are consumed.
+template <typename T> struct Row32;
+template <> struct Row32<uint16_t> {
+    u32x4 r[4];
+    __device__ __forceinline__ void load(const uint16_t* p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = *(const u32x4*)(p + 8 * i);
+    }
+    template <int I> __device__ __forceinline__ float get() const {
+        const uint32_t w = r[I / 8][(I % 8) / 2];
+        return __uint_as_float(I % 2 ? w & 0xffff0000u : w << 16);
+    }
+};
+template <> struct Row32<float> {
+    f32x4 r[8];
+    __device__ __forceinline__ void load(const float* p) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) r[i] = *(const f32x4*)(p + 4 * i);
+    }
+    template <int I> __device__ __forceinline__ float get() const { return r[I / 4][I % 4]; }
+};
+// sum += x[i] * w[i] for the 32 elements in ascending order (product, then
+// sum, each rounded).  The products are independent and formed first; only
+// the adds are a dependent chain.
+template <typename XT, typename GT>
+__device__ __forceinline__ void mac32(float& sum, const Row32<XT>& x, const Row32<GT>& w) {
+    float p[32];
+    static_for<32>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        p[i] = mul_rn(x.template get<i>(), w.template get<i>());
+    });
+#pragma unroll
+    for (int i = 0; i < 32; i++) sum = add_rn(sum, p[i]);
+}
+// 32-element chunks in flight per lane: 8 (4 for fp32 x and gate, whose
+// chunks take twice the registers)
+template <typename XT, typename GT>
+constexpr int exact_ring() { return sizeof(XT) == 4 && sizeof(GT) == 4 ? 4 : 8; }
+
 // ---------------------------------------------------------------- exact
-// Block = 256 threads = 4 waves.  tpb tokens per block (tpb*E <= 256 when
-// E <= 256; for E > 256 tpb = 1 and lanes loop over experts).
+// Block = 128 threads (E <= 128) or 256.  tpb tokens per block (tpb*E <=
+// the block when E fits it; otherwise tpb = 1 and lanes loop over experts).
 template <typename XT, typename GT>
 __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__ x,
                                                           const GT* __restrict__ wg,
@@ -248,11 +301,39 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
         if (t < T) {
             const XT* xr = x + (size_t)t * D;
             const GT* wr = wg + (size_t)e * D;
-            // the reference's order (d ascending, multiply then add); the
-            // operands arrive eight at a time (16-byte loads) when the rows
-            // are 16-byte aligned -- the dependent adds, not the loads, are
-            // then the critical path
+            // the reference's order (d ascending, multiply then add).  When
+            // the rows are 16-byte aligned the operands arrive 32 at a time
+            // through a ring of chunks in registers: a chunk's loads are
+            // issued 4-8 chunks before it is summed (one
+            // HBM latency is ~4000 cycles, one chunk's sum ~200), so the
+            // dependent adds, not the load latency, are the critical path (a
+            // lane waiting for each chunk's loads took 182 us for the
+            // Mixtral gate, T=4096, D=4096).  The ring's loads are issued
+            // unconditionally (chunks past the row re-read its last chunk)
+            // so every wait has the same count.
             int d = 0;
+            const int n32 = vec ? D / 32 : 0;  // uniform
+            if (n32 > 0) {
+                constexpr int kExactRing = exact_ring<XT, GT>();
+                Row32<XT> xc[kExactRing];
+                Row32<GT> wc[kExactRing];
+                static_for<kExactRing>([&](auto jc) __attribute__((always_inline)) {
+                    constexpr int jj = decltype(jc)::value;
+                    const int c = min(jj, n32 - 1);
+                    xc[jj].load(xr + 32 * c);
+                    wc[jj].load(wr + 32 * c);
+                });
+                for (int c0 = 0; c0 < n32; c0 += kExactRing) {
+                    static_for<kExactRing>([&](auto jc) __attribute__((always_inline)) {
+                        constexpr int jj = decltype(jc)::value;
+                        if (c0 + jj < n32) mac32(sum, xc[jj], wc[jj]);  // uniform
+                        const int cn = min(c0 + jj + kExactRing, n32 - 1);
+                        xc[jj].load(xr + 32 * cn);
+                        wc[jj].load(wr + 32 * cn);
+                    });
+                }
+                d = 32 * n32;
+            }
             if (vec) {
                 for (; d + 8 <= D; d += 8) {
                     float xv[8], wv[8];
@@ -300,11 +381,21 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
 // route_topk_kernel: one wave per token: sums the chunk partials in chunk
 //   order, then softmax + replace-min top-K + renormalisation
 //   (wave_route_token_reg).
+// LDS: an 8-stage ring of x slabs (64 tokens x 64 columns, 8 KB) and a
+// 3-stage ring of gate slabs (256 experts x 64 columns, 32 KB).  x comes from
+// HBM (every element is read by one block), the gate from L2 (the blocks of
+// a K-chunk share it), so x is loaded 7 K-steps ahead and the gate 2: 56 KB
+// of x in flight per CU, 14 MB over the chip, which the HBM latency needs
+// (with x and the gate in one 2-ahead ring, 16 KB of x per CU was in flight
+// and the gate GEMM ran at ~2.4 TB/s).
 constexpr int kRtTok = 64;
 constexpr int kRtExp = 256;
-constexpr int kRtStage = (kRtTok + kRtExp) * 128;  // 40960
-constexpr int kRtNS = 3;
-constexpr int kRtLds = kRtNS * kRtStage;           // 122880
+constexpr int kRtXStage = kRtTok * 128;            // 8192
+constexpr int kRtWStage = kRtExp * 128;            // 32768
+constexpr int kRtNX = 8;
+constexpr int kRtNW = 3;
+constexpr int kRtWOff = kRtNX * kRtXStage;         // 65536
+constexpr int kRtLds = kRtWOff + kRtNW * kRtWStage;  // 163840
 constexpr int kRtMinBlocks = 256;                  // one per CU
 constexpr int kRtMaxSplit = 16;                    // partials summed per logit (one wave per token)
 // Decode-sized batches (one 64-token tile) split the gate into up to 64
@@ -380,13 +471,22 @@ __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __res
         int k = kt + kt0;
         return k >= nloc ? k - nloc : k;
     };
-    auto issue = [&](int st, int kt) {
-        uint8_t* base = smem + st * kRtStage;
-        const int soff = (kb0 + kloc(kt)) * 128;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16, voff_x, soff, 0, 0);
+    // every issue is unconditional (a K-step past the chunk reads zeros into
+    // a stage nobody reads again), so each wait below has a fixed count
+    auto issue_x = [&](int kt) {
+        uint8_t* base = smem + (kt % kRtNX) * kRtXStage;
+        const bool live = kt < nloc;
+        const int soff = live ? (kb0 + kloc(kt)) * 128 : 0;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + 8 * wave * 128), 16,
+                                                 live ? voff_x : kOob, soff, 0, 0);
+    };
+    auto issue_w = [&](int kt) {
+        uint8_t* base = smem + kRtWOff + (kt % kRtNW) * kRtWStage;
+        const bool live = kt < nloc;
+        const int soff = live ? (kb0 + kloc(kt)) * 128 : 0;
         for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (lds_ptr_t)(base + (kRtTok + 32 * wave + 8 * j) * 128), 16, voff_w[j], soff, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + (32 * wave + 8 * j) * 128), 16,
+                                                     live ? voff_w[j] : kOob, soff, 0, 0);
     };
 
     const int q = lane >> 4, r16 = lane & 15;
@@ -401,14 +501,20 @@ __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __res
     float qv[8];
     float qam = 0.0f;
 
-    issue(0, 0);
-    if (nloc > 1) issue(1, 1);
+    // issue order: x(0..6), gate(0), gate(1), then per K-step kt: x(kt+7),
+    // gate(kt+2).  Waiting for x(kt) and gate(kt) leaves the 4 loads of
+    // gate(1) outstanding at kt = 0 and the 5 of step kt-1 after that.
+    for (int j = 0; j < kRtNX - 1; j++) issue_x(j);
+    issue_w(0);
+    issue_w(1);
     for (int kt = 0; kt < nloc; kt++) {
-        if (kt + 1 < nloc) wait_vmcnt<5>();
-        else wait_vmcnt<0>();
-        bare_barrier();
-        if (kt + 2 < nloc) issue((kt + 2) % kRtNS, kt + 2);
-        const uint8_t* base = smem + (kt % kRtNS) * kRtStage;
+        if (kt == 0) wait_vmcnt<4>();
+        else wait_vmcnt<5>();
+        bare_barrier();  // step kt landed; steps kt-1 (x, gate) and their stages free
+        issue_x(kt + kRtNX - 1);
+        issue_w(kt + 2);
+        const uint8_t* base = smem + (kt % kRtNX) * kRtXStage;
+        const uint8_t* wbase = smem + kRtWOff + (kt % kRtNW) * kRtWStage;
         u32x4 alo[4], ahi[4];
         for (int rt = 0; rt < 4; rt++) {
             const uint8_t* p = base + (16 * rt + r16) * 128;
@@ -416,7 +522,7 @@ __global__ __launch_bounds__(512) void route_logits_kernel(const uint16_t* __res
             ahi[rt] = *(const u32x4*)(p + off_hi);
         }
         for (int ct = 0; ct < 2; ct++) {
-            const uint8_t* p = base + (kRtTok + 32 * wave + 16 * ct + r16) * 128;
+            const uint8_t* p = wbase + (32 * wave + 16 * ct + r16) * 128;
             const u32x4 blo = *(const u32x4*)(p + off_lo), bhi = *(const u32x4*)(p + off_hi);
             for (int rt = 0; rt < 4; rt++) {
                 acc[rt][ct] = mfma_bf16(alo[rt], blo, acc[rt][ct]);
@@ -495,7 +601,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (lane + 64 * j < E) v[j] = add_rn(v[j], pv[i][j]);
-    wave_route_token_reg<KMAX>(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
+    wave_route_token_reg<KMAX, false>(v, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
 // route_topk_block_kernel: one 256-thread workgroup per token for gates
@@ -528,14 +634,18 @@ __global__ __launch_bounds__(256) void route_topk_block_kernel(const float* __re
     float r[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) r[j] = lane + 64 * j < E ? s_logit[lane + 64 * j] : -FLT_MAX;
-    wave_route_token_reg<KMAX>(r, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
+    wave_route_token_reg<KMAX, false>(r, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
 }
 
 // ---------------------------------------------------------------- launch
 template <typename XT, typename GT>
 int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int E, int K, int D,
                        int* idx, float* wts, hipStream_t st) {
-    int tpb = E <= 256 ? 256 / E : 1;
+    // 128-thread blocks for E <= 128: the (token, expert) lanes of a token
+    // batch then spread over twice the CUs, halving each CU's load volume
+    // (every lane streams its x row and gate row through the CU)
+    const int threads = E <= 128 ? 128 : 256;
+    int tpb = E <= threads ? threads / E : 1;
     if (tpb > 64) tpb = 64;
     size_t lds = sizeof(float) * (size_t)tpb * E;
     AMDMOE_CHECK_ARG(lds <= 64 * 1024, "routing: E=%d too large for the exact gate", E);
@@ -543,7 +653,7 @@ int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int 
     // every row 16-byte aligned: base pointers aligned, rows a multiple of 16 bytes
     const bool vec = ((uintptr_t)x & 15) == 0 && ((uintptr_t)wg & 15) == 0 && (D * sizeof(XT)) % 16 == 0 &&
                      (D * sizeof(GT)) % 16 == 0;
-    hipLaunchKernelGGL((route_exact_kernel<XT, GT>), dim3(grid), dim3(256), lds, st, x, wg, bias,
+    hipLaunchKernelGGL((route_exact_kernel<XT, GT>), dim3(grid), dim3(threads), lds, st, x, wg, bias,
                        T, E, K, D, tpb, vec, idx, wts);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;

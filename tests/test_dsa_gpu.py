@@ -84,13 +84,16 @@ def test_dsa_bf16_paged_baseline_shape(amd, orc):
 
 
 # H a multiple of 128: the token-split kernel (workgroup = query x 128 heads
-# x split) plus the merge of the splits
+# x split) plus the merge of the splits; H = 32, 64: one workgroup per
+# (query, 32 heads)
 @pytest.mark.parametrize("Q,H,S,ctx", [
-    (8, 128, 100, 512),    # 4 splits of 32, the last one 4 tokens
-    (3, 128, 1, 128),      # one token
-    (2, 256, 3000, 4096),  # 2 head groups; 64 splits of 64 tokens, the last 17 empty
-    (300, 128, 64, 128),   # one split per query (no token split)
-    (64, 128, 512, 1024),  # 4 splits of 4 tiles
+    (8, 128, 100, 512),     # 4 splits of 32, the last one 4 tokens
+    (3, 128, 1, 128),       # one token
+    (2, 256, 3000, 4096),   # 2 head groups; 64 splits of 64 tokens, the last 17 empty
+    (300, 128, 64, 128),    # one split per query (no token split)
+    (64, 128, 512, 1024),   # 4 splits of 4 tiles
+    (256, 32, 1, 128),      # 32 heads, one position
+    (128, 64, 2047, 4096),  # 64 heads, 64-token tiles, the last one ragged
 ])
 def test_dsa_bf16_paged_split_shapes(amd, orc, Q, H, S, ctx):
     print(f"dsa_bf16 split Q={Q} H={H} S={S}", flush=True)
@@ -157,6 +160,7 @@ def _invalid_mix(logical, pt, ctx, page, rng, all_invalid_q=None):
     (6, 128, 300, 1024),   # the token-split kernel (H % 128 == 0)
     (5, 64, 200, 1024),    # one workgroup per 32 heads, 64-token tiles (S <= 2048)
     (3, 32, 2500, 4096),   # one workgroup per 32 heads, 32-token tiles (S > 2048)
+    (64, 128, 300, 1024),  # the token-split kernel at the BASELINE query count (4 splits)
 ])
 def test_dsa_bf16_paged_invalid_indices(amd, orc, Q, H, S, ctx):
     """Selected positions that select nothing take no part in the softmax:
