@@ -331,26 +331,40 @@ def sweep(amdmoe, synth, iters, only=None):
         del x, wg, w1, w2, y, ws
     bf16_cfgs = [("medium_bf16_bias", (512, 8, 2, 1024, 2048), True)]
     bf16_cfgs += [(f"mixtral_bf16_T{T}", (T, 8, 2, 4096, 14336), False) for T in (16, 256, 4096)]
-    layer = None
+    layer, packed = None, None
     for name, (T, E, K, D, I), bias in bf16_cfgs:
-        if not want(name):
+        # the Mixtral rows come in both weight layouts: row-major (the
+        # reference's) and fragment-block packed (amdmoe_pack_weights_bf16)
+        lays = [(name, False)] + ([(name + "_packed", True)] if D == 4096 else [])
+        lays = [(n, pk) for n, pk in lays if want(n)]
+        if not lays:
             continue
         if layer is None or layer[0] != (E, D, I, bias) or layer[1].shape[0] < T:
-            layer = None
+            layer, packed = None, None
             torch.cuda.empty_cache()
             Tg = 4096 if D == 4096 else T
             layer = ((E, D, I, bias),) + synth.bf16_layer(Tg, E, D, I, seed=7, bias=bias)
         xa, wg, b, w1, w2 = layer[1:]
+        if packed is None and any(pk for _, pk in lays):
+            packed = (torch.empty_like(w1), torch.empty_like(w2))
+            amdmoe.pack_weights_bf16(w1, packed[0])
+            amdmoe.pack_weights_bf16(w2, packed[1])
         x = xa[:T].contiguous()
         y = torch.empty((T, D), dtype=torch.int16, device="cuda")
         cfg = amdmoe.moe_config(T, E, K, D, I)
         ws = amdmoe.alloc_workspace(cfg, amdmoe.AMDMOE_DTYPE_BF16)
         act = active_experts(lambda i, w: amdmoe.moe_gate_bf16x(x, wg, b, i, w, cfg), T, E, K)
-        ms = _time_calls(lambda: amdmoe.moe_forward_bf16(x, wg, b, w1, w2, y, cfg, ws=ws), iters)
-        row(name, "bf16", T, E, K, D, I, ms, act * 3 * I * D * 2 + E * D * 4,
-            2 * T * D * 2, 2.5e15, act)
+        for n, pk in lays:
+            if pk:
+                fwd = lambda: amdmoe.moe_forward_bf16_packed(x, wg, b, packed[0], packed[1], y, cfg,
+                                                             ws=ws)
+            else:
+                fwd = lambda: amdmoe.moe_forward_bf16(x, wg, b, w1, w2, y, cfg, ws=ws)
+            ms = _time_calls(fwd, iters)
+            row(n, "bf16", T, E, K, D, I, ms, act * 3 * I * D * 2 + E * D * 4,
+                2 * T * D * 2, 2.5e15, act)
         del x, y, ws
-    layer = None
+    layer, packed = None, None
     torch.cuda.empty_cache()
     # DeepSeek-V3 fp8 block-scale, packed (headline layout) and row-major
     E, K, D, I = 256, 8, 7168, 2048

@@ -110,6 +110,17 @@ int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const f
                             const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* The bf16 layer with pre-packed expert weights.  No counterpart in the
+ * reference (whose moe_forward is fp32 only): the same computation and
+ * arguments as amdmoe_moe_forward_bf16, but W1 and W2 are given in the
+ * fragment-block order written by amdmoe_pack_weights_bf16, so each of the
+ * grouped GEMMs' weight loads reads 1 KB contiguous instead of 16 rows x
+ * 64 bytes.  Results are bit-identical to the row-major entry. */
+int amdmoe_moe_forward_bf16_packed(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                                   const uint16_t* w1_packed, const uint16_t* w2_packed, uint16_t* y,
+                                   const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 /* Full MoE layer, FP8 block-scale (BASELINE DeepSeek-V3 config).
  *   x bf16 [T,D] (quantised internally to e4m3 with one fp32 scale per token
  *   per 128 columns); gate_weight bf16 [E,D];
@@ -205,6 +216,14 @@ int amdmoe_moe_forward_fp8_packed_noalloc(const uint16_t* x, const uint16_t* gat
  * rows % 16 == 0 and cols % 128 == 0; out must not alias w. */
 int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int cols, uint8_t* out,
                             void* stream);
+
+/* The same repacking for bf16 expert weights [num_experts][rows][cols]
+ * (W1 [E,2I,D] or W2 [E,D,I], naive_moe.cuh:66-72): the blocks are those of
+ * amdmoe_pack_weights_fp8 over the rows' 2*cols bytes (a 128-byte K-step
+ * holds 64 elements).  Needs rows % 16 == 0 and cols % 64 == 0; out must
+ * not alias w.  Feeds amdmoe_moe_forward_bf16_packed. */
+int amdmoe_pack_weights_bf16(const uint16_t* w, int num_experts, int rows, int cols, uint16_t* out,
+                             void* stream);
 
 /* --- stage entry points with the reference's semantics --- */
 

@@ -18,10 +18,11 @@ AMDMOE_DTYPE_MXFP4 = 3
 # Exported symbols, in the order include/amdmoe.h declares them.
 SYMBOLS = [
     "amdmoe_last_error", "amdmoe_version", "amdmoe_moe_workspace_bytes",
-    "amdmoe_moe_forward_f32", "amdmoe_moe_forward_f32_bias", "amdmoe_moe_forward_bf16", "amdmoe_moe_forward_fp8",
+    "amdmoe_moe_forward_f32", "amdmoe_moe_forward_f32_bias", "amdmoe_moe_forward_bf16",
+    "amdmoe_moe_forward_bf16_packed", "amdmoe_moe_forward_fp8",
     "amdmoe_moe_forward_fp8_packed", "amdmoe_moe_forward_mxfp4", "amdmoe_quant_weight_mxfp4",
     "amdmoe_quant_rows_mxfp8", "amdmoe_pack_weights_mxfp4", "amdmoe_moe_forward_fp8_packed_noalloc",
-    "amdmoe_pack_weights_fp8",
+    "amdmoe_pack_weights_fp8", "amdmoe_pack_weights_bf16",
     "amdmoe_moe_gate_f32", "amdmoe_moe_gate_bf16x", "amdmoe_moe_gate_bf16", "amdmoe_moe_gate_fp8",
     "amdmoe_moe_gather_f32", "amdmoe_moe_permute", "amdmoe_naive_gemm_f32",
     "amdmoe_swiglu_f32", "amdmoe_moe_scatter_f32", "amdmoe_quant_rows_fp8",
@@ -74,6 +75,7 @@ def load():
         "amdmoe_moe_forward_f32": (I, [_P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_f32_bias": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_bf16": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
+        "amdmoe_moe_forward_bf16_packed": (I, [_P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_fp8_packed": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
         "amdmoe_moe_forward_mxfp4": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P, SZ, _P]),
@@ -82,6 +84,7 @@ def load():
         "amdmoe_pack_weights_mxfp4": (I, [_P, _P, I, I, I, _P, _P, _P]),
         "amdmoe_moe_forward_fp8_packed_noalloc": (I, [_P, _P, _P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_pack_weights_fp8": (I, [_P, I, I, I, _P, _P]),
+        "amdmoe_pack_weights_bf16": (I, [_P, I, I, I, _P, _P]),
         "amdmoe_moe_gate_f32": (I, [_P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16x": (I, [_P, _P, _P, _P, _P, cfgp, _P]),
         "amdmoe_moe_gate_bf16": (I, [_P, _P, _P, _P, cfgp, _P]),
@@ -172,6 +175,20 @@ def moe_forward_bf16(x, wg, bias, w1, w2, y, cfg, ws=None, stream=None):
     p, n = _ws(ws)
     _check(load().amdmoe_moe_forward_bf16(_ptr(x), _ptr(wg), _ptr(bias), _ptr(w1), _ptr(w2),
                                           _ptr(y), ctypes.byref(cfg), p, n, _stream(stream)))
+
+
+def moe_forward_bf16_packed(x, wg, bias, w1p, w2p, y, cfg, ws=None, stream=None):
+    """amdmoe_moe_forward_bf16 with W1/W2 in pack_weights_bf16 order."""
+    p, n = _ws(ws)
+    _check(load().amdmoe_moe_forward_bf16_packed(_ptr(x), _ptr(wg), _ptr(bias), _ptr(w1p), _ptr(w2p),
+                                                 _ptr(y), ctypes.byref(cfg), p, n, _stream(stream)))
+
+
+def pack_weights_bf16(w, out, stream=None):
+    """Repack bf16 expert weights w [E, rows, cols] (int16 bit-view device tensor) into out
+    (same shape) in fragment-block order."""
+    E, rows, cols = w.shape
+    _check(load().amdmoe_pack_weights_bf16(_ptr(w), E, rows, cols, _ptr(out), _stream(stream)))
 
 
 def moe_forward_fp8(x, wg, w1, w1s, w2, w2s, y, cfg, ws=None, stream=None):

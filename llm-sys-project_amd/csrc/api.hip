@@ -323,10 +323,9 @@ int amdmoe_moe_forward_f32_bias(const float* x, const float* gate_weight, const 
                        stream);
 }
 
-int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
-                            const uint16_t* w1, const uint16_t* w2, uint16_t* y,
-                            const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+static int forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                        const uint16_t* w1, const uint16_t* w2, uint16_t* y, const MoeConfig* cfg,
+                        void* workspace, size_t workspace_bytes, void* stream, bool packed) {
     TRY(check_cfg(cfg, AMDMOE_DTYPE_BF16));
     const MoeConfig& c = *cfg;
     if (c.num_tokens == 0) return AMDMOE_OK;
@@ -341,7 +340,23 @@ int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const f
     TRY(mark(1, st));
     TRY(mark(2, st));
     return moe_experts(DT_BF16, c, w, (const uint8_t*)x, nullptr, (const uint8_t*)w1, nullptr,
-                       (const uint8_t*)w2, nullptr, y, st);
+                       (const uint8_t*)w2, nullptr, y, st, packed);
+}
+
+int amdmoe_moe_forward_bf16(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                            const uint16_t* w1, const uint16_t* w2, uint16_t* y,
+                            const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    return forward_bf16(x, gate_weight, gate_bias, w1, w2, y, cfg, workspace, workspace_bytes, stream,
+                        false);
+}
+
+int amdmoe_moe_forward_bf16_packed(const uint16_t* x, const float* gate_weight, const float* gate_bias,
+                                   const uint16_t* w1_packed, const uint16_t* w2_packed, uint16_t* y,
+                                   const MoeConfig* cfg, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    return forward_bf16(x, gate_weight, gate_bias, w1_packed, w2_packed, y, cfg, workspace,
+                        workspace_bytes, stream, true);
 }
 
 static int forward_fp8(const uint16_t* x, const uint16_t* gate_weight, const uint8_t* w1,
@@ -483,6 +498,16 @@ int amdmoe_pack_weights_fp8(const uint8_t* w, int num_experts, int rows, int col
                             void* stream) {
     AMDMOE_CHECK_ARG(w && out, "null tensor pointer");
     return launch_pack_weights(w, num_experts, rows, cols, out, (hipStream_t)stream);
+}
+
+int amdmoe_pack_weights_bf16(const uint16_t* w, int num_experts, int rows, int cols, uint16_t* out,
+                             void* stream) {
+    AMDMOE_CHECK_ARG(w && out, "null tensor pointer");
+    AMDMOE_CHECK_ARG(cols >= 0 && cols <= (1 << 29), "pack_weights_bf16: cols=%d out of range", cols);
+    // the fragment blocks are byte blocks: a bf16 row of cols elements is
+    // 2 cols bytes, one 128-byte K-step per 64 elements
+    return launch_pack_weights((const uint8_t*)w, num_experts, rows, 2 * cols, (uint8_t*)out,
+                               (hipStream_t)stream);
 }
 
 int amdmoe_moe_gate_f32(const float* x, const float* gate_weight, int* expert_indices,

@@ -16,13 +16,15 @@ int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hip
                      "grouped gemm: an operand exceeds 4 GiB (A %ld, expert %ld bytes)", g.a_bytes,
                      g.b_expert_bytes);
     AMDMOE_CHECK_ARG((dt != DT_FP8 && dt != DT_MX) || g.K / 128 <= kMaxKb, "grouped gemm: K=%d too large for fp8 / MX", g.K);
-    AMDMOE_CHECK_ARG(!g.b_packed || dt == DT_FP8 || dt == DT_MX, "grouped gemm: packed weights are fp8 / MX only");
+    AMDMOE_CHECK_ARG(!g.b_packed || dt == DT_FP8 || dt == DT_MX || dt == DT_BF16, "grouped gemm: packed weights are fp8 / bf16 / MX only");
     AMDMOE_CHECK_ARG(dt != DT_MX || g.b_packed, "grouped gemm: MX weights must be packed");
     AMDMOE_CHECK_ARG(dt != DT_MX || g.b_mx_scale_expert_bytes <= lim, "grouped gemm: MX scales exceed 2 GiB");
     if (dt == DT_MX) return mode == MODE_UP ? launch_gemm_variant<DT_MX, MODE_UP, true>(g, max_tiles, st)
                                             : launch_gemm_variant<DT_MX, MODE_DOWN, true>(g, max_tiles, st);
     if (dt == DT_F32) return mode == MODE_UP ? launch_gemm_variant<DT_F32, MODE_UP, false>(g, max_tiles, st)
                                              : launch_gemm_variant<DT_F32, MODE_DOWN, false>(g, max_tiles, st);
+    if (dt == DT_BF16 && g.b_packed) return mode == MODE_UP ? launch_gemm_variant<DT_BF16, MODE_UP, true>(g, max_tiles, st)
+                                                             : launch_gemm_variant<DT_BF16, MODE_DOWN, true>(g, max_tiles, st);
     if (dt == DT_BF16) return mode == MODE_UP ? launch_gemm_variant<DT_BF16, MODE_UP, false>(g, max_tiles, st)
                                               : launch_gemm_variant<DT_BF16, MODE_DOWN, false>(g, max_tiles, st);
     if (g.b_packed) return mode == MODE_UP ? launch_gemm_variant<DT_FP8, MODE_UP, true>(g, max_tiles, st)

@@ -946,6 +946,8 @@ AMDMOE_GEMM_VARIANT(DT_F32, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_F32, MODE_DOWN, false)
 AMDMOE_GEMM_VARIANT(DT_BF16, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_BF16, MODE_DOWN, false)
+AMDMOE_GEMM_VARIANT(DT_BF16, MODE_UP, true)
+AMDMOE_GEMM_VARIANT(DT_BF16, MODE_DOWN, true)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, true)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, false)

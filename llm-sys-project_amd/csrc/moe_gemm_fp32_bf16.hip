@@ -1,4 +1,4 @@
-// Grouped GEMM kernel variants: <DT_F32, MODE_UP, row-major>, <DT_F32, MODE_DOWN, row-major>, <DT_BF16, MODE_UP, row-major>, <DT_BF16, MODE_DOWN, row-major>.
+// Grouped GEMM kernel variants: fp32 UP / DOWN (row-major weights), bf16 UP / DOWN (row-major and packed weights).
 #include "moe_gemm.hpp"
 
 namespace amdmoe {
@@ -7,5 +7,7 @@ template int launch_gemm_variant<DT_F32, MODE_UP, false>(const GemmArgs&, long, 
 template int launch_gemm_variant<DT_F32, MODE_DOWN, false>(const GemmArgs&, long, hipStream_t);
 template int launch_gemm_variant<DT_BF16, MODE_UP, false>(const GemmArgs&, long, hipStream_t);
 template int launch_gemm_variant<DT_BF16, MODE_DOWN, false>(const GemmArgs&, long, hipStream_t);
+template int launch_gemm_variant<DT_BF16, MODE_UP, true>(const GemmArgs&, long, hipStream_t);
+template int launch_gemm_variant<DT_BF16, MODE_DOWN, true>(const GemmArgs&, long, hipStream_t);
 
 }  // namespace amdmoe

@@ -710,7 +710,14 @@ def test_forward_every_tile_group_f32_bf16(amd, orc, dtype):
         xb, w1b, w2b = orc.f32_to_bf16(x), orc.f32_to_bf16(w1), orc.f32_to_bf16(w2)
         y = torch.empty((T, D), dtype=torch.int16, device="cuda")
         amd.moe_forward_bf16(dev(xb), dev(wg), None, dev(w1b), dev(w2b), y, cfg)
+        # the packed-weight entry on every tile group: bit-identical
+        p1, p2 = torch.empty_like(dev(w1b)), torch.empty_like(dev(w2b))
+        amd.pack_weights_bf16(dev(w1b), p1)
+        amd.pack_weights_bf16(dev(w2b), p2)
+        yp = torch.empty_like(y)
+        amd.moe_forward_bf16_packed(dev(xb), dev(wg), None, p1, p2, yp, cfg)
         torch.cuda.synchronize()
+        assert torch.equal(yp, y)
         idx_r, _, y_ref = orc.moe_forward_bf16(xb, wg, w1b, w2b, K)
         err = np.abs(orc.bf16_to_f32(bf16_np(y)) - y_ref).max()
         bar = 2.0 ** -7 * np.abs(y_ref).max()
@@ -788,6 +795,39 @@ def test_forward_bf16_mixtral_t4096_tile_edges(amd, orc):
     assert n_edge >= 40
     err, y_ref, yg = _bf16_case(amd, orc, T, E, K, D, I, bias=False, sample=rows, seed=7)
     assert bf16_bar_ok(yg, y_ref)
+
+
+def test_pack_weights_bf16_is_the_byte_packing(amd):
+    """pack_weights_bf16 lays out a bf16 row's 2*cols bytes exactly as
+    pack_weights_fp8 lays out a row of that many bytes (whose format
+    test_pack_weights_format checks)."""
+    w = torch.randint(-32768, 32767, (3, 48, 320), dtype=torch.int16, device="cuda")
+    a = torch.empty_like(w)
+    b = torch.empty((3, 48, 640), dtype=torch.uint8, device="cuda")
+    amd.pack_weights_bf16(w, a)
+    amd.pack_weights_fp8(w.view(torch.uint8), b)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.uint8), b)
+
+
+def test_forward_bf16_packed_bit_identical_mixtral_t256(amd):
+    """Mixtral shape (112 N-tiles of UP, 16 of DOWN, experts of ~64 rows):
+    the packed-weight bf16 forward equals the row-major one bit for bit."""
+    import synth
+    T, E, K, D, I = 256, 8, 2, 4096, 14336
+    announce("forward_bf16_packed mixtral T=256")
+    x, wg, _, w1, w2 = synth.bf16_layer(T, E, D, I, seed=7, bias=False)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    yp = torch.empty_like(y)
+    amd.moe_forward_bf16(x, wg, None, w1, w2, y, cfg)
+    p1, p2 = torch.empty_like(w1), torch.empty_like(w2)
+    amd.pack_weights_bf16(w1, p1)
+    amd.pack_weights_bf16(w2, p2)
+    del w1, w2
+    amd.moe_forward_bf16_packed(x, wg, None, p1, p2, yp, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(yp, y)
 
 
 def test_forward_bf16_mixtral_t256(amd, orc):
