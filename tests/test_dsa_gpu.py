@@ -101,6 +101,31 @@ def test_dsa_bf16_paged_split_shapes(amd, orc, Q, H, S, ctx):
     assert _paged_case(amd, orc, Q, H, S, ctx, check_q=check, seed=Q + S) < 1e-2
 
 
+def test_dsa_bf16_paged_repeat_calls_bit_identical(amd):
+    """Calls of different split counts and head groups in a row (sharing
+    the decode's cached scratch of partials), each shape's output
+    bit-identical across its calls."""
+    import synth
+    shapes = [(64, 128, 512, 1024), (8, 128, 100, 512), (2, 256, 3000, 4096), (300, 128, 64, 128)]
+    cases = []
+    for i, (Q, H, S, ctx) in enumerate(shapes):
+        inp = synth.dsa_paged(Q, H, 512, 64, S, 64, ctx, seed=30 + i)
+        cfg = amd.dsa_config(Q, H, 512, 64, S, 64, Q * ctx)
+        cases.append((inp, cfg, torch.empty((Q, H, 512), dtype=torch.int16, device="cuda")))
+    first = []
+    for rnd in range(3):
+        for i, (inp, cfg, out) in enumerate(cases):
+            print(f"dsa_bf16 repeat round {rnd} shape {shapes[i]}", flush=True)
+            qn, qp, cache, pt, logical, pps = inp
+            out.fill_(-1)
+            amd.dsa_decode_bf16_paged(qn, qp, cache, pt, logical, out, cfg, pps)
+            torch.cuda.synchronize()
+            if rnd == 0:
+                first.append(out.clone())
+            else:
+                assert torch.equal(out, first[i]), shapes[i]
+
+
 def test_dsa_bf16_paged_split_max_jumps(amd, orc):
     """Scores that jump by more than 8 (log2 units) between tiles of a split:
     the path that moves O out of the accumulators and rescales it in memory.
