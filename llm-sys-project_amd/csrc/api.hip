@@ -58,6 +58,20 @@ struct MoeWs {
 static int elem_size(int dtype) { return dtype == AMDMOE_DTYPE_F32 ? 4 : (dtype == AMDMOE_DTYPE_BF16 ? 2 : 1); }
 static bool is_8bit(int dtype) { return dtype == AMDMOE_DTYPE_FP8 || dtype == AMDMOE_DTYPE_MXFP4; }
 
+// K splits of the fp32 / bf16 down projection.  Its work items are (M-tile,
+// 256-column N-tile) pairs; with few experts and a long I (Mixtral: 8
+// experts x 16 N-tiles x 4-5 M-tiles = 512-640 items of 224 K-steps) they
+// fill the 256 CUs only two-and-a-bit times, so the last round runs on a
+// fraction of the chip.  Splitting I in two doubles the items and halves
+// each; the two fp32 partial rows of a slot are added in the combine.
+static int down_splits(const MoeConfig& c, int dtype) {
+    if (is_8bit(dtype)) return 1;
+    const long P = (long)c.num_tokens * c.top_k;
+    const long items = max_mtiles(P, c.num_experts) * ceil_div((long)c.hidden_dim, 256L);
+    const long nk = (long)c.intermediate_dim * elem_size(dtype) / 128;  // K-steps
+    return items <= 1024 && nk >= 32 && nk % 2 == 0 ? 2 : 1;
+}
+
 // Lays the workspace out from `base` (nullptr: sizes only).
 static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     MoeWs w{};
@@ -92,9 +106,10 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
         w.logits = (float*)take(route_mfma_scratch_bytes((int)T, (int)E, (int)D, dtype == AMDMOE_DTYPE_FP8));
     } else {
         // the down-projection's weighted rows stay fp32 on the fp32 and bf16
-        // paths, so a bf16 output is rounded once (in the combine)
+        // paths, so a bf16 output is rounded once (in the combine); one set
+        // of rows per K split
         w.act = take(elem_size(dtype) * P * I);
-        w.ypair = take(4 * P * D);
+        w.ypair = take(4 * P * D * (size_t)down_splits(c, dtype));
     }
     w.total = off;
     return w;
@@ -261,10 +276,14 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.out = w.ypair;
     dn.sorted_slot = w.sorted_slot;
     dn.sorted_w = w.sorted_w;
+    const int nsplit = dt == DT_F32 ? down_splits(c, AMDMOE_DTYPE_F32)
+                                    : (dt == DT_BF16 ? down_splits(c, AMDMOE_DTYPE_BF16) : 1);
+    dn.k_splits = nsplit;
+    dn.out_split_stride = P * D;
     TRY(launch_grouped_gemm(dt, MODE_DOWN, dn, mtiles, st));
     TRY(mark(5, st));
     TRY(launch_combine(dt == DT_F32 || dt == DT_BF16 ? DT_F32 : DT_BF16, dt == DT_F32 ? DT_F32 : DT_BF16,
-                       w.ypair, w.idx, T, K, E, D, y, st));
+                       w.ypair, w.idx, T, K, E, D, y, st, nsplit));
     return mark(6, st);
 }
 

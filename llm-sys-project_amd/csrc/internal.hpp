@@ -54,6 +54,10 @@ struct GemmArgs {
     long out_scale_rows;     // UP fp8 / MX: dwords per 128-column block of out_scale
     const int* sorted_slot;  // DOWN: flat slot t*K+k of each sorted row
     const float* sorted_w;   // DOWN: routing weight of each sorted row
+    int k_splits;            // DOWN with fp32 rows (fp32 / bf16): K split over this many work
+                             // items (0 or 1: none); split s writes its partial rows at
+                             // out + s * out_split_stride floats
+    long out_split_stride;
     // MX only: E8M0 weight scales in fragment order [E][b_rows/16][K/128][64]
     // (a_scale then holds the activations' E8M0 scales, four bytes -- the
     // 32-blocks of a 128-K step -- per dword)
@@ -123,9 +127,10 @@ int launch_pack_mxfp4(const uint8_t* q, const uint8_t* s, long E, int N, int K, 
 // K % 128 == 0)
 int launch_pack_weights(const uint8_t* w, long E, long N, long K, uint8_t* out, hipStream_t st);
 
-// moe_combine.hip: ypair rows fp32 or bf16 (DT_F32 / DT_BF16), y fp32 or bf16
+// moe_combine.hip: ypair rows fp32 or bf16 (DT_F32 / DT_BF16), y fp32 or bf16;
+// nsplit fp32 partial row sets of T*K*D floats each (a split down projection)
 int launch_combine(int ypair_dt, int out_dt, const void* ypair, const int* idx, int T, int K, int E,
-                   int D, void* y, hipStream_t st);
+                   int D, void* y, hipStream_t st, int nsplit = 1);
 int launch_naive_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
                           hipStream_t st);
 int launch_swiglu_f32(const float* gate, const float* up, float* out, int n, hipStream_t st);

@@ -31,10 +31,14 @@ template <> struct Vec8<uint16_t> {
     }
 };
 
+// nsp > 1 (fp32 rows of a down projection whose K was split): a slot's row
+// is the sum of its nsp partial rows, sp_stride elements apart, added in
+// split order before it joins the expert-order sum.
 template <typename PT, bool OUT_BF16>
 __global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypair,
                                                       const int* __restrict__ idx, int T, int K,
-                                                      int E, int D, void* __restrict__ y) {
+                                                      int E, int D, void* __restrict__ y, int nsp,
+                                                      size_t sp_stride) {
     __shared__ int s_ord[64];
     __shared__ int s_n;
     const int t = blockIdx.x;
@@ -61,7 +65,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const PT* __restrict__ ypa
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         for (int j = 0; j < n; j++) {
             float v[8];
-            Vec8<PT>::load(ypair + ((size_t)t * K + s_ord[j]) * D + 8 * c, v);
+            const PT* src = ypair + ((size_t)t * K + s_ord[j]) * D + 8 * c;
+            Vec8<PT>::load(src, v);
+            for (int sp = 1; sp < nsp; sp++) {
+                float u[8];
+                Vec8<PT>::load(src + sp * sp_stride, u);
+                for (int i = 0; i < 8; i++) v[i] = add_rn(v[i], u[i]);
+            }
             for (int i = 0; i < 8; i++) acc[i] = add_rn(acc[i], v[i]);
         }
         if (OUT_BF16) {
@@ -154,17 +164,20 @@ __global__ __launch_bounds__(256) void combine_bf16_kernel(const uint16_t* __res
 }
 
 int launch_combine(int ypair_dt, int out_dt, const void* ypair, const int* idx, int T, int K, int E,
-                   int D, void* y, hipStream_t st) {
+                   int D, void* y, hipStream_t st, int nsplit) {
     AMDMOE_CHECK_ARG(K <= 64 && D % 8 == 0, "combine: K=%d D=%d unsupported", K, D);
     AMDMOE_CHECK_ARG(ypair_dt == DT_F32 || out_dt == DT_BF16, "combine: bf16 rows need a bf16 output");
+    AMDMOE_CHECK_ARG(nsplit >= 1 && (nsplit == 1 || ypair_dt == DT_F32), "combine: %d partial row sets need fp32 rows",
+                     nsplit);
+    const size_t sp_stride = (size_t)T * K * D;
     if (T == 0) return AMDMOE_OK;
     if (ypair_dt == DT_F32 && out_dt == DT_F32)
         hipLaunchKernelGGL((combine_kernel<float, false>), dim3(T), dim3(256), 0, st,
-                           (const float*)ypair, idx, T, K, E, D, y);
+                           (const float*)ypair, idx, T, K, E, D, y, nsplit, sp_stride);
     else if (ypair_dt == DT_F32)
         // fp32 rows, bf16 output (the bf16 layer): the sum is rounded once
         hipLaunchKernelGGL((combine_kernel<float, true>), dim3(T), dim3(256), 0, st,
-                           (const float*)ypair, idx, T, K, E, D, y);
+                           (const float*)ypair, idx, T, K, E, D, y, nsplit, sp_stride);
     else if (D <= 8 * 256 * 4 && T <= 64)
         // few tokens: a token's columns over several workgroups (one 8-column
         // group per thread), so no CU streams a whole token's K rows alone
@@ -175,7 +188,7 @@ int launch_combine(int ypair_dt, int out_dt, const void* ypair, const int* idx, 
                            idx, T, K, E, D, (uint16_t*)y);
     else
         hipLaunchKernelGGL((combine_kernel<uint16_t, true>), dim3(T), dim3(256), 0, st,
-                           (const uint16_t*)ypair, idx, T, K, E, D, y);
+                           (const uint16_t*)ypair, idx, T, K, E, D, y, 1, sp_stride);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }

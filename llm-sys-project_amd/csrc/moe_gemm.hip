@@ -18,6 +18,14 @@ int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hip
     AMDMOE_CHECK_ARG((dt != DT_FP8 && dt != DT_MX) || g.K / 128 <= kMaxKb, "grouped gemm: K=%d too large for fp8 / MX", g.K);
     AMDMOE_CHECK_ARG(!g.b_packed || dt == DT_FP8 || dt == DT_MX || dt == DT_BF16, "grouped gemm: packed weights are fp8 / bf16 / MX only");
     AMDMOE_CHECK_ARG(dt != DT_MX || g.b_packed, "grouped gemm: MX weights must be packed");
+    {
+        const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);
+        const long nk = (long)g.K * es / 128;
+        AMDMOE_CHECK_ARG(g.k_splits <= 1 || (mode == MODE_DOWN && (dt == DT_F32 || dt == DT_BF16) &&
+                                             nk % g.k_splits == 0 && g.out_split_stride > 0),
+                         "grouped gemm: a K split (%d) needs DOWN with fp32 rows and whole K-steps per split",
+                         g.k_splits);
+    }
     AMDMOE_CHECK_ARG(dt != DT_MX || g.b_mx_scale_expert_bytes <= lim, "grouped gemm: MX scales exceed 2 GiB");
     if (dt == DT_MX) return mode == MODE_UP ? launch_gemm_variant<DT_MX, MODE_UP, true>(g, max_tiles, st)
                                             : launch_gemm_variant<DT_MX, MODE_DOWN, true>(g, max_tiles, st);

@@ -207,7 +207,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
 
     // ---- work item (XCD-chunked) ----
-    const int W = (*g.num_tiles) * g.n_tiles_n;
+    // DOWN with fp32 rows may split K over S items per (M-tile, N-tile):
+    // virtual N-tile v = S * nt + ks (uniform)
+    constexpr bool kCanSplit = MODE == MODE_DOWN && (DT == DT_F32 || DT == DT_BF16);
+    const int S = kCanSplit ? max(g.k_splits, 1) : 1;
+    const int W = (*g.num_tiles) * g.n_tiles_n * S;
     const int per = (W + 7) >> 3;
     const int slot = blockIdx.x >> 3;
     if (slot >= per) return;
@@ -217,18 +221,21 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // tile), ordered N-tile major: item f*ntn + m*nt + j is (tile f+j, nt),
     // so the m tiles that read the same weight tile are dispatched back to
     // back on one XCD and share its weight stream through L2.
-    const int ntn = g.n_tiles_n;
+    const int ntn = g.n_tiles_n * S;
     const int mt0 = w / ntn;  // a tile of the owning expert
     const int4 tile0 = g.tiles[mt0];
     const int m_tiles = tile0.w & 0xffff, first_tile = mt0 - (tile0.w >> 16);
     const int l_item = w - first_tile * ntn;
-    const int nt = __builtin_amdgcn_readfirstlane(l_item / m_tiles);
-    const int mt = first_tile + (l_item - nt * m_tiles);
+    const int ntv = __builtin_amdgcn_readfirstlane(l_item / m_tiles);
+    const int mt = first_tile + (l_item - ntv * m_tiles);
+    const int nt = S == 1 ? ntv : ntv / S, ks = ntv - nt * S;
     const int4 tile = m_tiles == 1 ? tile0 : g.tiles[mt];
     // uniform values (SGPRs): the asm loads take their soffsets from them
     const int e = __builtin_amdgcn_readfirstlane(tile.x), row0 = __builtin_amdgcn_readfirstlane(tile.y),
               rows = __builtin_amdgcn_readfirstlane(tile.z);
-    const int nk = (int)((long)g.K * ES / 128);
+    const int nk_all = (int)((long)g.K * ES / 128);  // K-steps of the whole reduction
+    const int nk = nk_all / S;                          // K-steps of this item: [ks nk, ks nk + nk)
+    const int kbase = ks * nk;
     const int kb_per_row = g.K / 128;  // fp8 scale blocks along K
 
     // ---- buffer descriptors ----
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
         voff_b[ct] = ok ? (uint32_t)nb : kOob;
         // MX: E8M0 scales of the 16 rows' K-step, [lane] bytes per block of 64
-        voff_bs[ct] = ok ? (uint32_t)((n - r16) / 16 * nk * 64 + lane) : kOob;
+        voff_bs[ct] = ok ? (uint32_t)((n - r16) / 16 * nk_all * 64 + lane) : kOob;
     }
     __builtin_amdgcn_sched_barrier(0);
     int row_slot = 0;
@@ -335,7 +342,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     auto kblk = [&](int kt) __attribute__((always_inline)) {
         int k = kt + kt0;
         k = k >= nk ? k - nk : k;
-        return k >= nk ? k - nk : k;
+        return kbase + (k >= nk ? k - nk : k);
     };
 
     // Loads for a K-step past the end (kt >= nk) are still issued, through
@@ -872,7 +879,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 for (int ct = 0; ct < 2; ct++) {
                     const int n = nt * 256 + 32 * wave + 16 * ct + 4 * q;
                     if (n >= g.n_out) continue;
-                    *(f32x4*)((float*)g.out + sl * g.n_out + n) = acc[rt][ct] * wgt;
+                    *(f32x4*)((float*)g.out + ks * g.out_split_stride + sl * g.n_out + n) = acc[rt][ct] * wgt;
                 }
             }
         } else {
@@ -929,7 +936,7 @@ int launch_gemm_variant(const GemmArgs& g, long max_tiles, hipStream_t st) {
         const int rc = ensure_dynamic_lds((const void*)grouped_gemm_kernel<DT, MODE, PK>, kGemmLds);
         if (rc != AMDMOE_OK) return rc;
     }
-    long work = max_tiles * g.n_tiles_n;
+    long work = max_tiles * g.n_tiles_n * (MODE == MODE_DOWN && (DT == DT_F32 || DT == DT_BF16) ? max(g.k_splits, 1) : 1);
     long grid = 8 * ceil_div(work, 8);
     if (grid == 0) return AMDMOE_OK;
     AMDMOE_CHECK_ARG(grid < (1L << 31), "grouped gemm: grid too large (%ld)", grid);

@@ -357,6 +357,160 @@ __global__ __launch_bounds__(256) void route_exact_kernel(const XT* __restrict__
     }
 }
 
+// ------------------------------------------------------- exact, LDS-fed
+// route_exact_lds_kernel: the same per-(token, expert) sequential sums as
+// route_exact_kernel (mac32: d ascending, product then sum, each rounded),
+// for an fp32 gate, E in {2, 4, 8, 16} and D a multiple of 256 (fp32 x with
+// E = 2 excepted: its stages do not fit three deep).  One wave per block holds
+// 64/E tokens x E experts.  The block's x rows and the whole gate stream
+// through LDS in 256-element stages: a ring of NST stages, the global -> LDS
+// DMA of stage c + NST - 1 issued before stage c is summed.  Each x and gate
+// row then crosses L2 -> CU once per block instead of once per lane, and
+// NST - 1 stages (5 at the Mixtral gate: 1280 elements, ~8000 cycles of
+// adds) are in flight where a lane's register ring held ~4 chunks of 32 --
+// short of the load latency, so the dependent adds waited on loads (90-100
+// us for the Mixtral gate at T = 256 and at T = 4096).  A row's 16-byte
+// pieces sit at piece ^ (row & 15), so the distinct rows one read touches
+// (64/E of x, E of the gate) fall on distinct banks.
+constexpr int kXch = 256;  // elements per stage
+
+template <typename XT, typename GT, int E>
+struct ExactLds {
+    static constexpr int XB = kXch * (int)sizeof(XT);   // bytes of an x row per stage
+    static constexpr int GB = kXch * (int)sizeof(GT);   // bytes of a gate row per stage
+    static constexpr int TPB = 64 / E;                  // tokens per block
+    static constexpr int XBYTES = TPB * XB;
+    static constexpr int STAGE = XBYTES + E * GB;
+    static constexpr int NLD = STAGE / 1024;            // DMA instructions per stage
+    static constexpr int NST0 = 73728 / STAGE < 8 ? 73728 / STAGE : 8;
+    static constexpr int NST = NST0 < 63 / NLD + 1 ? NST0 : 63 / NLD + 1;  // (NST - 1) * NLD <= 63
+    static constexpr int LDS = NST * STAGE + 64 * 4;    // + the block's logits
+    // whole DMA instructions per region, at least two stages in flight
+    static constexpr bool OK = XBYTES % 1024 == 0 && (E * GB) % 1024 == 0 && NST >= 3;
+};
+
+// A Row32's k-th 16-byte vector (its elements 16k/sizeof(T) .. in order).
+__device__ __forceinline__ void set16(Row32<uint16_t>& r, int k, u32x4 v) { r.r[k] = v; }
+__device__ __forceinline__ void set16(Row32<float>& r, int k, u32x4 v) { r.r[k] = __builtin_bit_cast(f32x4, v); }
+
+// The body is a device template behind plain kernels (below): the host side
+// emits no launch stub for a kernel template instantiated this way.
+template <typename XT, typename GT, int E>
+__device__ __forceinline__ void route_exact_lds_body(const XT* __restrict__ x, const GT* __restrict__ wg,
+                                                     const float* __restrict__ bias, int T, int K, int D,
+                                                     int* __restrict__ idx, float* __restrict__ wts) {
+    using L = ExactLds<XT, GT, E>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* s_logit = (float*)(smem + L::NST * L::STAGE);
+    const int lane = threadIdx.x;
+    const int t0 = blockIdx.x * L::TPB;
+    const int nst = D / kXch;  // stages of the row
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (long)T * D * (long)sizeof(XT));
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wg, (long)E * D * (long)sizeof(GT));
+    // DMA instruction n of a stage: this lane's 16 bytes land at LDS offset
+    // 1024 n + 16 lane of the stage; the piece it loads is the one that
+    // offset holds under the XOR layout (stage c adds c * kXch elements)
+    uint32_t voff[L::NLD];
+#pragma unroll
+    for (int n = 0; n < L::NLD; n++) {
+        const int o = 1024 * n + 16 * lane;
+        if (1024 * n < L::XBYTES) {
+            const int row = o / L::XB, piece = ((o % L::XB) >> 4) ^ (row & 15);
+            const long t = min(t0 + row, T - 1);  // rows past T re-read the last token
+            voff[n] = (uint32_t)(t * D * (long)sizeof(XT) + 16 * piece);
+        } else {
+            const int ow = o - L::XBYTES;
+            const int row = ow / L::GB, piece = ((ow % L::GB) >> 4) ^ (row & 15);
+            voff[n] = (uint32_t)((long)row * D * (long)sizeof(GT) + 16 * piece);
+        }
+    }
+    auto issue = [&](int c) __attribute__((always_inline)) {
+        const int cc = min(c, nst - 1);  // stages past the row re-read its last one
+        uint8_t* st = smem + (c % L::NST) * L::STAGE;
+#pragma unroll
+        for (int n = 0; n < L::NLD; n++) {
+            if (1024 * n < L::XBYTES)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(st + 1024 * n), 16, voff[n],
+                                                         cc * kXch * (int)sizeof(XT), 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + 1024 * n), 16, voff[n],
+                                                         cc * kXch * (int)sizeof(GT), 0, 0);
+        }
+    };
+    const int lt = lane / E, e = lane % E;
+    constexpr int XP = 32 * (int)sizeof(XT) / 16, GP = 32 * (int)sizeof(GT) / 16;  // pieces per 32 elements
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < L::NST - 1; c++) issue(c);
+    for (int c = 0; c < nst; c++) {
+        issue(c + L::NST - 1);        // into the stage summed at c - 1 (its reads are done)
+        wait_vmcnt<(L::NST - 1) * L::NLD>();  // stage c has landed
+        const uint8_t* st = smem + (c % L::NST) * L::STAGE;
+        const uint8_t* xs = st + lt * L::XB;
+        const uint8_t* ws = st + L::XBYTES + e * L::GB;
+#pragma unroll
+        for (int s32 = 0; s32 < kXch / 32; s32++) {
+            Row32<XT> xr;
+            Row32<GT> wr;
+            // Row32 holds its 32 elements as 16-byte vectors in order
+#pragma unroll
+            for (int k = 0; k < XP; k++) set16(xr, k, *(const u32x4*)(xs + 16 * ((s32 * XP + k) ^ (lt & 15))));
+#pragma unroll
+            for (int k = 0; k < GP; k++) set16(wr, k, *(const u32x4*)(ws + 16 * ((s32 * GP + k) ^ (e & 15))));
+            mac32(sum, xr, wr);
+        }
+    }
+    wait_vmcnt<0>();  // the trailing re-reads
+    if (bias) sum = add_rn(sum, bias[e]);
+    s_logit[lane] = sum;
+    __syncthreads();
+    for (int j = 0; j < L::TPB; j++) {
+        const int t = t0 + j;
+        if (t >= T) break;
+        wave_route_token(s_logit + j * E, E, K, idx + (size_t)t * K, wts + (size_t)t * K);
+    }
+}
+
+template <typename XT, typename GT, int E> struct ExactLdsKernel {
+    static constexpr void (*fn)(const XT*, const GT*, const float*, int, int, int, int*, float*) = nullptr;
+};
+#define AMDMOE_EXACT_LDS_KERNEL(NAME, XT, GT, E)                                                            \
+    __global__ __launch_bounds__(64) void NAME(const XT* __restrict__ x, const GT* __restrict__ wg,         \
+                                               const float* __restrict__ bias, int T, int K, int D,         \
+                                               int* __restrict__ idx, float* __restrict__ wts) {            \
+        route_exact_lds_body<XT, GT, E>(x, wg, bias, T, K, D, idx, wts);                                     \
+    }                                                                                                        \
+    template <> struct ExactLdsKernel<XT, GT, E> {                                                           \
+        static constexpr void (*fn)(const XT*, const GT*, const float*, int, int, int, int*, float*) = NAME; \
+    };
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_f32_f32_e4, float, float, 4)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_f32_f32_e8, float, float, 8)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_f32_f32_e16, float, float, 16)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_bf16_f32_e2, uint16_t, float, 2)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_bf16_f32_e4, uint16_t, float, 4)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_bf16_f32_e8, uint16_t, float, 8)
+AMDMOE_EXACT_LDS_KERNEL(route_exact_lds_bf16_f32_e16, uint16_t, float, 16)
+// (a bf16 gate whose D is a multiple of 64 routes on the MFMA path)
+#undef AMDMOE_EXACT_LDS_KERNEL
+
+// -1: this (types, E) has no LDS-fed form (its stages do not fit three deep)
+template <typename XT, typename GT, int E>
+static int launch_exact_lds(const XT* x, const GT* wg, const float* bias, int T, int K, int D, int* idx,
+                            float* wts, hipStream_t st) {
+    using L = ExactLds<XT, GT, E>;
+    constexpr auto kern = ExactLdsKernel<XT, GT, E>::fn;
+    if constexpr (!L::OK || kern == nullptr) {
+        return -1;
+    } else {
+        const int rc = ensure_dynamic_lds((const void*)kern, L::LDS);
+        if (rc != AMDMOE_OK) return rc;
+        hipLaunchKernelGGL(kern, dim3((unsigned)ceil_div(T, L::TPB)), dim3(64), L::LDS, st, x, wg, bias, T, K, D, idx,
+                           wts);
+        AMDMOE_LAUNCH_CHECK();
+        return AMDMOE_OK;
+    }
+}
+
 // ---------------------------------------------------------------- MFMA
 // bf16 x [T,D] and bf16 Wg [E,D], E <= 256, D % 64 == 0.  Two launches:
 //
@@ -653,6 +807,20 @@ int launch_route_exact(const XT* x, const GT* wg, const float* bias, int T, int 
     // every row 16-byte aligned: base pointers aligned, rows a multiple of 16 bytes
     const bool vec = ((uintptr_t)x & 15) == 0 && ((uintptr_t)wg & 15) == 0 && (D * sizeof(XT)) % 16 == 0 &&
                      (D * sizeof(GT)) % 16 == 0;
+    // the LDS-fed form: few experts, whole 256-element stages, x and the gate
+    // within a buffer descriptor's 32-bit range
+    if (vec && T > 0 && D % kXch == 0 && K <= 16 && (long)T * D * (long)sizeof(XT) < (1L << 31) &&
+        (long)E * D * (long)sizeof(GT) < (1L << 31)) {
+        int rc = -1;
+        switch (E) {
+            case 2: rc = launch_exact_lds<XT, GT, 2>(x, wg, bias, T, K, D, idx, wts, st); break;
+            case 4: rc = launch_exact_lds<XT, GT, 4>(x, wg, bias, T, K, D, idx, wts, st); break;
+            case 8: rc = launch_exact_lds<XT, GT, 8>(x, wg, bias, T, K, D, idx, wts, st); break;
+            case 16: rc = launch_exact_lds<XT, GT, 16>(x, wg, bias, T, K, D, idx, wts, st); break;
+            default: break;
+        }
+        if (rc != -1) return rc;
+    }
     hipLaunchKernelGGL((route_exact_kernel<XT, GT>), dim3(grid), dim3(threads), lds, st, x, wg, bias,
                        T, E, K, D, tpb, vec, idx, wts);
     AMDMOE_LAUNCH_CHECK();

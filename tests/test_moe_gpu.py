@@ -187,6 +187,35 @@ def test_gate_bf16_mfma_random_margin_aware(amd, orc, T):
     np.testing.assert_allclose(gw[ok], wts_ref[ok], rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("xt", ["f32", "bf16"])
+@pytest.mark.parametrize("E,K,T,D", [(2, 1, 77, 768), (4, 2, 130, 512), (8, 2, 1000, 4096), (16, 4, 33, 1280),
+                                     (8, 2, 4096, 256)])
+def test_gate_fp32_weights_lds_path(amd, orc, xt, E, K, T, D):
+    """The fp32-gate routing with E in {2, 4, 8, 16} and D a multiple of 256
+    (x rows and the gate staged through LDS; fp32 x with E = 2 takes the
+    per-lane kernel): the reference's sequential fp32 logits, so indices
+    equal the oracle's exactly.  T leaves a ragged last block; D = 256 is a
+    single stage, D = 768 / 1280 an odd count of stages."""
+    announce(f"gate exact {xt} E={E} K={K} T={T} D={D}")
+    rng = np.random.default_rng(E * 1000 + T)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    wg = (rng.standard_normal((E, D)) / np.sqrt(D)).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    cfg = amd.moe_config(T, E, K, D, 64)
+    if xt == "f32":
+        idx_ref, wts_ref = orc.moe_route(x, wg, K)
+        amd.moe_gate_f32(dev(x), dev(wg), idx, wts, cfg)
+    else:
+        xb = orc.f32_to_bf16(x)
+        idx_ref, wts_ref = orc.moe_route(orc.bf16_to_f32(xb), wg, K, bias=b)
+        amd.moe_gate_bf16x(dev(xb), dev(wg), dev(b), idx, wts, cfg)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(idx), idx_ref)
+    np.testing.assert_allclose(host(wts), wts_ref, rtol=2e-6)
+
+
 def test_gate_bias_and_bf16x(amd, orc):
     T, E, K, D = 128, 8, 2, 1024
     rng = np.random.default_rng(13)
@@ -685,15 +714,17 @@ def test_forward_fp8_every_token_tile_count(amd, orc, dsv3):
     assert rel < 2e-2
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_forward_every_tile_group_f32_bf16(amd, orc, dtype):
+@pytest.mark.parametrize("dtype,I", [("f32", 256), ("bf16", 256), ("f32", 2048), ("bf16", 2048)])
+def test_forward_every_tile_group_f32_bf16(amd, orc, dtype, I):
     """fp32 and bf16 main loops are instantiated per group of four 16-row
     tiles (4, 8, 12, 16): routing fixed through the gate gives experts every
     row count of ROUTED_COUNTS (all four groups, split experts); full output
-    against the oracle at the fp32 / bf16 bars."""
+    against the oracle at the fp32 / bf16 bars.  I = 2048 (32 / 64 K-steps)
+    runs the down projection with its K split in two (partial rows added
+    in the combine)."""
     T, chosen = _routed_layout(ROUTED_COUNTS, 64, 2)
-    E, K, D, I = 64, 2, 128, 256
-    announce(f"forward_{dtype} every tile group: T={T}")
+    E, K, D = 64, 2, 128
+    announce(f"forward_{dtype} every tile group: T={T} I={I}")
     rng = np.random.default_rng(1250)
     x, wg = _routing_columns(chosen, E, D, rng)
     w1 = (rng.standard_normal((E, 2 * I, D)) / np.sqrt(D)).astype(np.float32)
