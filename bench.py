@@ -513,7 +513,7 @@ def stats_summary(csv_dir, out_md, title, command):
              "|---|---:|---:|---:|---:|---:|"]
     for r in csv.DictReader(open(files[0])):
         k = kernel_label(r["Name"])
-        if k.startswith("at::") or k.startswith("rocprim") or "elementwise" in k:
+        if not k or k.startswith("at::") or k.startswith("rocprim") or "elementwise" in k:
             continue
         lines.append(f"| `{k}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
@@ -553,16 +553,53 @@ def pmc_summary(csv_dir, out_md, title, command):
             agg[k]["duration_us"].append(dur[(k, _d)])
     if dur:
         counters.append("duration_us")
+    # derived columns, where their counters were collected:
+    #   clock GHz   = GRBM_GUI_ACTIVE / 8 (one count per XCD) / duration
+    #   MFMA busy   = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs)
+    #   MFMA TF/s   = (SQ_INSTS_VALU_MFMA_MOPS_F8 + _BF16) x 512 / duration
+    #   LDS conflict = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS
+    #   L2 hit      = TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
+    derived = []
+    have = set(counters)
+    if {"GRBM_GUI_ACTIVE", "duration_us"} <= have:
+        derived.append(("clock GHz", lambda a: a["GRBM_GUI_ACTIVE"] / 8 / a["duration_us"] / 1e3))
+    if {"GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES"} <= have:
+        derived.append(("MFMA busy", lambda a: a["SQ_VALU_MFMA_BUSY_CYCLES"] / (a["GRBM_GUI_ACTIVE"] / 8 * 1024)))
+    mops = [c for c in ("SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_BF16") if c in have]
+    if mops and "duration_us" in have:
+        derived.append(("MFMA TF/s", lambda a: sum(a[c] for c in mops) * 512 / (a["duration_us"] * 1e-6) / 1e12))
+    if {"SQ_LDS_BANK_CONFLICT", "SQ_ACTIVE_INST_LDS"} <= have:
+        derived.append(("LDS conflict", lambda a: a["SQ_LDS_BANK_CONFLICT"] / max(a["SQ_ACTIVE_INST_LDS"], 1.0)))
+    if {"TCC_HIT_sum", "TCC_MISS_sum"} <= have:
+        derived.append(("L2 hit", lambda a: a["TCC_HIT_sum"] / max(a["TCC_HIT_sum"] + a["TCC_MISS_sum"], 1.0)))
     lines = [f"# {title}", "", "Command (from the repository root on the GPU box):", "", "```",
              command, "```", "",
              "Per kernel: each counter summed over its hardware instances per dispatch, averaged "
-             "over the kernel's dispatches.", "",
-             "| kernel | dispatches | " + " | ".join(counters) + " |",
-             "|---|---:|" + "---:|" * len(counters)]
+             "over the kernel's dispatches."]
+    if derived:
+        lines += ["", "Derived: clock GHz = GRBM_GUI_ACTIVE / 8 (one count per XCD) / duration; "
+                  "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs); "
+                  "MFMA TF/s = MFMA_MOPS x 512 / duration (padded rows included); LDS conflict = "
+                  "SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS; L2 hit = TCC_HIT / (TCC_HIT + TCC_MISS).  "
+                  "For kernels of a few microseconds GRBM_GUI_ACTIVE also counts the dispatch, so their "
+                  "clock column reads high.  Rows: this library's kernels (torch and rocprim kernels of "
+                  "the synthetic-data setup omitted)."]
+    lines += ["", "| kernel | dispatches | " + " | ".join(counters + [d[0] for d in derived]) + " |",
+              "|---|---:|" + "---:|" * (len(counters) + len(derived))]
     for k in sorted(agg, key=lambda k: -max(sum(v) for v in agg[k].values())):
+        if not k or k.startswith("at::") or k.startswith("rocprim"):
+            continue  # torch / rocprim kernels of the synthetic-data setup
         n = max(len(v) for v in agg[k].values())
-        vals = [sum(agg[k][c]) / len(agg[k][c]) if agg[k][c] else float("nan") for c in counters]
-        lines.append(f"| `{k}` | {n} | " + " | ".join(f"{v:.4g}" for v in vals) + " |")
+        avg = {c: sum(agg[k][c]) / len(agg[k][c]) if agg[k][c] else float("nan") for c in counters}
+        vals = [avg[c] for c in counters]
+        dv = []
+        for name, f in derived:
+            try:
+                x = f(avg)
+                dv.append(f"{100 * x:.1f}%" if name in ("MFMA busy", "LDS conflict", "L2 hit") else f"{x:.3g}")
+            except (ZeroDivisionError, KeyError):
+                dv.append("-")
+        lines.append(f"| `{k}` | {n} | " + " | ".join([f"{v:.4g}" for v in vals] + dv) + " |")
     with open(out_md, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
