@@ -523,6 +523,7 @@ int amdmoe_pack_weights_bf16(const uint16_t* w, int num_experts, int rows, int c
                              void* stream) {
     AMDMOE_CHECK_ARG(w && out, "null tensor pointer");
     AMDMOE_CHECK_ARG(cols >= 0 && cols <= (1 << 29), "pack_weights_bf16: cols=%d out of range", cols);
+    AMDMOE_CHECK_ARG(cols % 64 == 0, "pack_weights_bf16: cols=%d must be a multiple of 64", cols);
     // the fragment blocks are byte blocks: a bf16 row of cols elements is
     // 2 cols bytes, one 128-byte K-step per 64 elements
     return launch_pack_weights((const uint8_t*)w, num_experts, rows, 2 * cols, (uint8_t*)out,

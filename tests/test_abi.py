@@ -104,3 +104,23 @@ def test_pack_weights_validates_before_device_work():
     assert b"128" in lib.amdmoe_last_error()
     assert lib.amdmoe_pack_weights_fp8(p, 1, 16, 128, p, None) == 1
     assert b"in-place" in lib.amdmoe_last_error()
+
+
+def test_pack_weights_bf16_validates_before_device_work():
+    lib = amdmoe.load()
+    p = ctypes.c_void_p(4096)
+    assert lib.amdmoe_pack_weights_bf16(None, 1, 16, 64, p, None) == 1
+    assert b"null" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_bf16(p, 1, 16, 96, ctypes.c_void_p(8192), None) == 1
+    assert b"multiple of 64" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_bf16(p, 1, 24, 64, ctypes.c_void_p(8192), None) == 1
+    assert b"16" in lib.amdmoe_last_error()
+    assert lib.amdmoe_pack_weights_bf16(p, 1, 16, 64, p, None) == 1
+    assert b"in-place" in lib.amdmoe_last_error()
+    # the packed bf16 forward checks its configuration and pointers like the row-major one
+    cfg = amdmoe.moe_config(4, 4, 2, 96, 128)
+    rc = lib.amdmoe_moe_forward_bf16_packed(None, None, None, None, None, None, ctypes.byref(cfg), None, 0, None)
+    assert rc == 1 and b"multiples of 64" in lib.amdmoe_last_error()
+    cfg = amdmoe.moe_config(4, 4, 2, 64, 128)
+    rc = lib.amdmoe_moe_forward_bf16_packed(None, None, None, None, None, None, ctypes.byref(cfg), None, 0, None)
+    assert rc == 1 and b"null" in lib.amdmoe_last_error()
