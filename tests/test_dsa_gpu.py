@@ -128,7 +128,7 @@ def test_dsa_bf16_paged_repeat_calls_bit_identical(amd):
 
 def test_dsa_bf16_paged_split_max_jumps(amd, orc):
     """Scores that jump by more than 8 (log2 units) between tiles of a split:
-    the path that moves O out of the accumulators and rescales it in memory.
+    the path that rescales O to a raised running max.
     Scores come from q_pe . K_p only (q_nope = 0), values from K_c: in every
     128-token split, tile 1 and tile 3 open with a token whose score is
     9.6 resp. 19.2 above the rest and whose V row is -1 (all other V rows
@@ -147,6 +147,34 @@ def test_dsa_bf16_paged_split_max_jumps(amd, orc):
         w[s0 + 96], vv[s0 + 96] = 5.0, -1.0   # tile 3: +19.2
     phys = torch.from_numpy(orc.dsa_translate(logical.cpu().numpy(), pt.cpu().numpy(), page)
                             .astype(np.int64)).cuda()          # [Q, S]
+    rows = torch.empty((Q, S, 576), dtype=torch.float32)
+    rows[:, :, :512] = vv[None, :, None]
+    rows[:, :, 512:] = w[None, :, None]
+    cache.index_copy_(0, phys.reshape(-1), rows.reshape(-1, 576).to(torch.bfloat16).view(torch.int16).cuda())
+    err = _paged_case(amd, orc, Q, H, S, ctx, page=page, check_q=[0, 31, 63],
+                      inputs=(qn, qp, cache, pt, logical, pps))
+    assert err < 1e-2
+
+
+def test_dsa_bf16_paged_split_large_jump(amd, orc):
+    """A tile max ~96 (log2 units) above the split's first tile max (a
+    rescale of O by 2^-96): even heads (q_pe = 1) meet tokens with K_p = 25
+    and 24.8 in split 2 (V = -1 and +1, so the output depends on both), odd
+    heads (q_pe = 0.1) a jump of ~9.6; every other position has score 0 and
+    V = 0.5."""
+    import synth
+    print("dsa_bf16 split large jump", flush=True)
+    Q, H, S, ctx, page = 64, 128, 512, 1024, 64
+    qn, qp, cache, pt, logical, pps = synth.dsa_paged(Q, H, 512, 64, S, page, ctx, seed=19)
+    qn = torch.zeros_like(qn)
+    qpe = torch.where(torch.arange(H) % 2 == 0, 1.0, 0.1)[None, :, None].expand(Q, H, 64)
+    qp = qpe.to(torch.bfloat16).view(torch.int16).contiguous().cuda()
+    w = torch.zeros(S)
+    vv = torch.full((S,), 0.5)
+    w[256 + 32], vv[256 + 32] = 25.0, -1.0
+    w[256 + 40], vv[256 + 40] = 24.8, 1.0
+    phys = torch.from_numpy(orc.dsa_translate(logical.cpu().numpy(), pt.cpu().numpy(), page)
+                            .astype(np.int64)).cuda()
     rows = torch.empty((Q, S, 576), dtype=torch.float32)
     rows[:, :, :512] = vv[None, :, None]
     rows[:, :, 512:] = w[None, :, None]
