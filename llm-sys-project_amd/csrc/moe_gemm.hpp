@@ -754,6 +754,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int r8 = 0; r8 < 8; r8++) {
                 const int rt = 8 * half + r8;
+                if (rt >= ntiles) continue;  // uniform: no live row in this tile
                 f32x4 hv;
                 for (int i = 0; i < 4; i++) {
                     const float gv = acc[rt][0][i], uv = acc[rt][1][i];
@@ -774,8 +775,12 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             }
             __syncthreads();
             const int rr = 128 * half + er;
+            // the four lanes of a row (one quad: the shuffles below stay in
+            // it) take the branch together; a wave past the live rows skips
+            // the reads, the requantisation and the stores
+            if (rr >= rows) continue;
             const int col = nt * 128 + 32 * pp;
-            const bool ok = rr < rows && col < g.n_out;
+            const bool ok = col < g.n_out;
             // eight unconditional 16-byte reads (the staged row is in LDS
             // whether or not it is stored), zeroed where not stored.  Parts
             // pp and pp + 2 of a row lie 128 bytes apart, on the same banks,
@@ -904,6 +909,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int r8 = 0; r8 < 8; r8++) {
                     const int rt = 8 * half + r8;
+                    if (rt >= ntiles) continue;  // uniform: no live row in this tile
                     const float wgt = s_wt[16 * rt + r16];
                     const f32x4 v0 = acc[rt][0] * wgt, v1 = acc[rt][1] * wgt;
                     const auto s0 = __builtin_amdgcn_permlane16_swap(pack_bf16x2(v0[0], v0[1]),
@@ -915,6 +921,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                 lds_barrier();
     #pragma unroll
                 for (int j = 0; j < 8; j++) {
+                    if (128 * half + 16 * j >= rows) break;  // uniform: rows 16j.. of the pass are past the tile
                     const int c = tid + 512 * j;       // 16-byte chunk of the pass
                     const int rr = c >> 5, ch = c & 31;  // row in the pass, chunk in the row
                     const int r = 128 * half + rr;
