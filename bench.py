@@ -420,6 +420,9 @@ def kernel_label(name):
         mode = ("UP", "DOWN")[int(m.group(2))]
         lay = "packed" if m.group(3) == "true" else "row-major"
         return f"grouped_gemm_kernel<{dt}, {mode}, {lay}>"
+    m = re.match(r"grouped_gemm_bf16_w4_kernel<(\d)>", base)
+    if m:
+        return f"grouped_gemm_bf16_w4_kernel<{('UP', 'DOWN')[int(m.group(1))]}>"
     m = re.match(r"indexer_topk_kernel<(\d+), (\d)>", base)
     if m:
         return f"indexer_topk_kernel<{m.group(1)}, {('full', 'part', 'merge')[int(m.group(2))]}>"

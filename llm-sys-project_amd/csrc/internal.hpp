@@ -107,6 +107,8 @@ int launch_quant_weight(const float* w, long rows, int cols, const float* u, uin
 // moe_gemm.hip
 long max_mtiles(long P, int E);
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
+// moe_gemm_bf16_w4.hip: the bf16 packed-weight GEMMs on one wave per SIMD
+int launch_gemm_bf16_w4(int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
 
 // moe_generic.hip: fp32 UP + DOWN + combine for any D and I (the forward's
 // tail when D or I is not a multiple of 32), over the permutation's M-tiles

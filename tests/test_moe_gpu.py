@@ -861,6 +861,55 @@ def test_forward_bf16_packed_bit_identical_mixtral_t256(amd):
     assert torch.equal(yp, y)
 
 
+def test_forward_bf16_packed_bit_identical_mixtral_t4096(amd):
+    """Mixtral T=4096 (four full 256-row M-tiles per expert, the down
+    projection split in two along I): the packed-weight bf16 forward (4
+    waves x 64 weight rows) equals the row-major one (8 waves x 32 rows)
+    bit for bit."""
+    import synth
+    T, E, K, D, I = 4096, 8, 2, 4096, 14336
+    announce("forward_bf16_packed mixtral T=4096")
+    x, wg, _, w1, w2 = synth.bf16_layer(T, E, D, I, seed=7, bias=False)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    yp = torch.empty_like(y)
+    amd.moe_forward_bf16(x, wg, None, w1, w2, y, cfg)
+    p1, p2 = torch.empty_like(w1), torch.empty_like(w2)
+    amd.pack_weights_bf16(w1, p1)
+    amd.pack_weights_bf16(w2, p2)
+    del w1, w2
+    amd.moe_forward_bf16_packed(x, wg, None, p1, p2, yp, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(yp, y)
+
+
+@pytest.mark.parametrize("T,D,I", [(300, 320, 192), (40, 192, 320)])
+def test_forward_bf16_packed_bit_identical_partial_tiles(amd, T, D, I):
+    """N-tiles cut short on both projections (I and D multiples of 64 but
+    not of 128 / 256: the last UP N-tile has 64 of its 128 columns, the
+    last DOWN N-tile 64 of 256), and M-tiles of every tile group: packed
+    equals row-major bit for bit."""
+    E, K = 16, 4
+    announce(f"forward_bf16_packed partial tiles T={T} D={D} I={I}")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1251)
+    x = (torch.randn((T, D), generator=g, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    wg = torch.randn((E, D), generator=g, device="cuda") / D ** 0.5
+    w1 = (torch.randn((E, 2 * I, D), generator=g, device="cuda") / D ** 0.5).to(torch.bfloat16).view(torch.int16)
+    w2 = (torch.randn((E, D, I), generator=g, device="cuda") / I ** 0.5).to(torch.bfloat16).view(torch.int16)
+    cfg = amd.moe_config(T, E, K, D, I)
+    y = torch.empty((T, D), dtype=torch.int16, device="cuda")
+    yp = torch.empty_like(y)
+    amd.moe_forward_bf16(x, wg, None, w1, w2, y, cfg)
+    p1, p2 = torch.empty_like(w1), torch.empty_like(w2)
+    amd.pack_weights_bf16(w1, p1)
+    amd.pack_weights_bf16(w2, p2)
+    amd.moe_forward_bf16_packed(x, wg, None, p1, p2, yp, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(yp, y)
+    assert bool(torch.isfinite(y.view(torch.bfloat16).float()).all())
+
+
 def test_forward_bf16_mixtral_t256(amd, orc):
     """BASELINE Mixtral config at T=256, every token checked (outputs reach
     |y| ~ 2.6, where bf16_bar_ok is the reference's 1e-2)."""
