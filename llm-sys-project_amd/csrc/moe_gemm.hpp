@@ -553,9 +553,6 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // Issue order per step: activation slots of step kt+2, then the 4
         // weight loads of step kt+RB-1.  Everything of step kt has landed
         // once at most kWait vector-memory instructions are outstanding:
-        //   RB == 5: the weights of steps kt+1..kt+3 (12), which also
-        //            covers the activations of step kt (they precede the
-        //            weights of steps kt+1..kt+3);
         //   RB == 3: the weights of step kt+1 (4), which follow the
         //            activations of step kt+1 (those are thus waited for
         //            one step early).
@@ -577,10 +574,10 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         //            kt the activations of step kt+1 (issued at step kt-1, the
         //            step's oldest loads) are written to LDS: only the scale
         //            and the 4 weight loads of step kt-1 may be outstanding.
-        static_assert(RB >= 2 && RB <= 5, "wait counts are derived for rings of 2 to 5 sets");
+        static_assert(RB >= 2 && RB <= 4, "wait counts are derived for rings of 2 to 4 sets");
         static_assert(!kVg || RB == 4, "the register path's wait count is derived for RB == 4");
         static_assert(!kVg1 || RB == 3, "the one-set register path's wait count is derived for RB == 3");
-        wait_vmcnt<kVg ? NS + 9 : (kVg1 ? 5 : (RB == 5 ? 12 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0))))>();
+        wait_vmcnt<kVg ? NS + 9 : (kVg1 ? 5 : (RB == 4 ? 8 : (RB == 3 ? 4 : 0)))>();
         // the weights of this step have landed: pin every use of them below
         // the wait (the loads were asm, invisible to the compiler's waits)
         pin(cur);
