@@ -31,9 +31,7 @@ int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hip
                                             : launch_gemm_variant<DT_MX, MODE_DOWN, true>(g, max_tiles, st);
     if (dt == DT_F32) return mode == MODE_UP ? launch_gemm_variant<DT_F32, MODE_UP, false>(g, max_tiles, st)
                                              : launch_gemm_variant<DT_F32, MODE_DOWN, false>(g, max_tiles, st);
-    if (dt == DT_BF16 && g.b_packed) return launch_gemm_bf16_w4(mode, g, max_tiles, st);
-    if (dt == DT_BF16) return mode == MODE_UP ? launch_gemm_variant<DT_BF16, MODE_UP, false>(g, max_tiles, st)
-                                              : launch_gemm_variant<DT_BF16, MODE_DOWN, false>(g, max_tiles, st);
+    if (dt == DT_BF16) return launch_gemm_bf16_w4(mode, g, max_tiles, st);
     if (g.b_packed) return mode == MODE_UP ? launch_gemm_variant<DT_FP8, MODE_UP, true>(g, max_tiles, st)
                                            : launch_gemm_variant<DT_FP8, MODE_DOWN, true>(g, max_tiles, st);
     return mode == MODE_UP ? launch_gemm_variant<DT_FP8, MODE_UP, false>(g, max_tiles, st)

@@ -45,7 +45,11 @@
 //
 // The kernel template lives in this header; each moe_gemm_<type>.hip file
 // instantiates some of its variants (the fp8 ones are large: one main loop
-// per live token-tile count), so they compile in parallel.
+// per live token-tile count), so they compile in parallel.  Built: fp8 and
+// MX (both projections), fp32.  The bf16 GEMMs run
+// grouped_gemm_bf16_w4_kernel (moe_gemm_bf16_w4.hip: same items and
+// arithmetic, 4 waves x 64 weight rows); the template's bf16 branches are
+// not instantiated.
 #pragma once
 
 #include <type_traits>
@@ -955,10 +959,6 @@ int launch_gemm_variant(const GemmArgs& g, long max_tiles, hipStream_t st) {
     extern template int launch_gemm_variant<DT, MODE, PK>(const GemmArgs&, long, hipStream_t);
 AMDMOE_GEMM_VARIANT(DT_F32, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_F32, MODE_DOWN, false)
-AMDMOE_GEMM_VARIANT(DT_BF16, MODE_UP, false)
-AMDMOE_GEMM_VARIANT(DT_BF16, MODE_DOWN, false)
-AMDMOE_GEMM_VARIANT(DT_BF16, MODE_UP, true)
-AMDMOE_GEMM_VARIANT(DT_BF16, MODE_DOWN, true)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, false)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_UP, true)
 AMDMOE_GEMM_VARIANT(DT_FP8, MODE_DOWN, false)

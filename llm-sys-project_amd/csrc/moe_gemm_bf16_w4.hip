@@ -1,12 +1,13 @@
-// Grouped GEMM for bf16 packed weights, one wave per SIMD: 4 waves x 64
-// weight rows per work item (the bf16 layers' GEMMs: Mixtral, the medium
-// bf16 configuration).
+// Grouped GEMM for bf16 weights (packed or row-major), one wave per SIMD:
+// 4 waves x 64 weight rows per work item (the bf16 layers' GEMMs: Mixtral,
+// the medium bf16 configuration).
 //
 // Work items, K-step order, weight fragments, activation slabs and the
-// arithmetic are those of grouped_gemm_kernel<DT_BF16, MODE, true> (same
-// bf16 16x16x32 MFMA, same operand lanes, same K-step rotation and the same
-// epilogue arithmetic), so the outputs are bit-identical to it; what differs
-// is the wave layout.  There every one of 8 waves multiplies 32 weight rows
+// arithmetic are those of the template grouped_gemm_kernel in moe_gemm.hpp
+// (same bf16 16x16x32 MFMA, same operand lanes, same K-step rotation and the
+// same epilogue arithmetic), whose bf16 instantiations it replaced with
+// bit-identical outputs; what differs is the wave layout.  There every one
+// of 8 waves multiplies 32 weight rows
 // by all of the tile's token rows, so each token fragment read from LDS
 // feeds 4 MFMAs: per 64-element K-step of a full M-tile a CU reads 8 x 32 KB
 // of fragments (2048 cycles at 128 B per clock) against 2048 MFMA cycles per
@@ -66,7 +67,11 @@ struct W4Step {
     uint8_t* st;
 };
 
-template <int MODE>
+// PK: weights in fragment-block order (pack_weights_bf16: each 16-row
+// group's K-step is 2 KB, [half][lane][16 B], one 1 KB load per half);
+// otherwise row-major (lane (q, r16) reads 16 bytes of row r16 at K offset
+// 16q, and 64 + 16q for the hi half)
+template <int MODE, bool PK>
 __global__ __launch_bounds__(kW4Threads, 1) void grouped_gemm_bf16_w4_kernel(GemmArgs g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -130,8 +135,8 @@ __global__ __launch_bounds__(kW4Threads, 1) void grouped_gemm_bf16_w4_kernel(Gem
             n = (long)nt * 256 + 64 * wave + 16 * ct + r16;
             ok = n < g.n_out;
         }
-        // fragment blocks: a 16-row group's K-step is 2 KB, [half][lane][16 B]
-        voff_b[ct] = ok ? (uint32_t)((n - r16) * g.b_row_bytes + 16 * lane) : kOob;
+        const long nb = PK ? (n - r16) * g.b_row_bytes + 16 * lane : n * g.b_row_bytes + 16 * q;
+        voff_b[ct] = ok ? (uint32_t)nb : kOob;
     }
     // DOWN: each row's slot and routing weight, only needed by the epilogue
     // (the loads stay in flight through the main loop)
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void grouped_gemm_bf16_w4_kernel(Gem
         s.ra = kta < nk ? ra : ra0;
         s.rb = ktb < nk ? rb : rb0;
         s.so_a = kblk(kta) * 128;
-        s.so_b = kblk(ktb) * 2048;
+        s.so_b = kblk(ktb) * (PK ? 2048 : 128);
         s.st = smem + (kta % kW4Ring) * kW4Stage;
         return s;
     };
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void grouped_gemm_bf16_w4_kernel(Gem
             } else {
                 constexpr int j = sl - NS, ct = j >> 1;
                 if constexpr (j & 1)
-                    f.q[ct][1] = buffer_load_b128_async<1024, MODE == MODE_DOWN>(s.rb, voff_b[ct], s.so_b);
+                    f.q[ct][1] = buffer_load_b128_async<PK ? 1024 : 64, MODE == MODE_DOWN>(s.rb, voff_b[ct], s.so_b);
                 else
                     f.q[ct][0] = buffer_load_b128_async<0, MODE == MODE_DOWN>(s.rb, voff_b[ct], s.so_b);
             }
@@ -355,8 +360,10 @@ __global__ __launch_bounds__(kW4Threads, 1) void grouped_gemm_bf16_w4_kernel(Gem
 }
 
 int launch_gemm_bf16_w4(int mode, const GemmArgs& g, long max_tiles, hipStream_t st) {
-    const void* fn = mode == MODE_UP ? (const void*)grouped_gemm_bf16_w4_kernel<MODE_UP>
-                                     : (const void*)grouped_gemm_bf16_w4_kernel<MODE_DOWN>;
+    const void* fn = mode == MODE_UP ? (g.b_packed ? (const void*)grouped_gemm_bf16_w4_kernel<MODE_UP, true>
+                                                   : (const void*)grouped_gemm_bf16_w4_kernel<MODE_UP, false>)
+                                     : (g.b_packed ? (const void*)grouped_gemm_bf16_w4_kernel<MODE_DOWN, true>
+                                                   : (const void*)grouped_gemm_bf16_w4_kernel<MODE_DOWN, false>);
     {
         const int rc = ensure_dynamic_lds(fn, kW4Lds);
         if (rc != AMDMOE_OK) return rc;
@@ -365,13 +372,8 @@ int launch_gemm_bf16_w4(int mode, const GemmArgs& g, long max_tiles, hipStream_t
     const long grid = 8 * ceil_div(work, 8);
     if (grid == 0) return AMDMOE_OK;
     AMDMOE_CHECK_ARG(grid < (1L << 31), "grouped gemm: grid too large (%ld)", grid);
-    if (mode == MODE_UP)
-        hipLaunchKernelGGL(grouped_gemm_bf16_w4_kernel<MODE_UP>, dim3((unsigned)grid), dim3(kW4Threads), kW4Lds,
-                           st, g);
-    else
-        hipLaunchKernelGGL(grouped_gemm_bf16_w4_kernel<MODE_DOWN>, dim3((unsigned)grid), dim3(kW4Threads),
-                           kW4Lds, st, g);
-    AMDMOE_LAUNCH_CHECK();
+    void* args[] = {(void*)&g};
+    AMDMOE_HIP_TRY(hipLaunchKernel(fn, dim3((unsigned)grid), dim3(kW4Threads), args, kW4Lds, st));
     return AMDMOE_OK;
 }
 
