@@ -58,18 +58,46 @@ struct MoeWs {
 static int elem_size(int dtype) { return dtype == AMDMOE_DTYPE_F32 ? 4 : (dtype == AMDMOE_DTYPE_BF16 ? 2 : 1); }
 static bool is_8bit(int dtype) { return dtype == AMDMOE_DTYPE_FP8 || dtype == AMDMOE_DTYPE_MXFP4; }
 
+// fp32 D and I the MFMA kernels tile (whole 32-element K steps); other
+// shapes take the bounds-checked kernels of moe_generic.hip
+static bool f32_mfma_shape(const MoeConfig& c) {
+    return c.hidden_dim % 32 == 0 && c.intermediate_dim % 32 == 0;
+}
+
+// M-tile rows.  The fp32 GEMMs are bound by MFMA work per CU, so a small
+// layer whose 256-row M-tiles give fewer than 256 UP work items (the medium
+// configuration: 8 experts of ~128 rows x 16 N-tiles = 128 items) leaves CUs
+// idle; halving the tile rows (down to 64) doubles its items.  The bf16,
+// fp8 and MX GEMMs stream weights, and keep 256 rows (fewer weight passes).
+static int mtile_rows(const MoeConfig& c, int dtype) {
+    if (dtype != AMDMOE_DTYPE_F32 || !f32_mfma_shape(c)) return kMTile;
+    const long P = (long)c.num_tokens * c.top_k;
+    const long up_ntiles = ceil_div((long)c.intermediate_dim, 128L);
+    int bm = kMTile;
+    while (bm > 64 && (P / bm) * up_ntiles < 256) bm /= 2;
+    return bm;
+}
+
 // K splits of the fp32 / bf16 down projection.  Its work items are (M-tile,
-// 256-column N-tile) pairs; with few experts and a long I (Mixtral: 8
+// 256-column N-tile) pairs.  With few experts and a long I (Mixtral: 8
 // experts x 16 N-tiles x 4-5 M-tiles = 512-640 items of 224 K-steps) they
 // fill the 256 CUs only two-and-a-bit times, so the last round runs on a
-// fraction of the chip.  Splitting I in two doubles the items and halves
-// each; the two fp32 partial rows of a slot are added in the combine.
+// fraction of the chip: I is split in two when there are at most 1024
+// items.  A small layer (the medium configuration: 8 experts x 4 N-tiles)
+// fills only part of the chip even then, so the splits keep doubling while
+// the items would not fill the 256 CUs once, each split keeping at least 8
+// whole K-steps, up to 8 splits.  The s fp32 partial rows of a slot are
+// added in the combine, in split order.  (More splits where the items
+// already fill the chip cost the partial rows' traffic: Mixtral T=256 with
+// 8 splits, 0.530 -> 0.587 ms.)
 static int down_splits(const MoeConfig& c, int dtype) {
     if (is_8bit(dtype)) return 1;
     const long P = (long)c.num_tokens * c.top_k;
-    const long items = max_mtiles(P, c.num_experts) * ceil_div((long)c.hidden_dim, 256L);
+    const long items = max_mtiles(P, c.num_experts, mtile_rows(c, dtype)) * ceil_div((long)c.hidden_dim, 256L);
     const long nk = (long)c.intermediate_dim * elem_size(dtype) / 128;  // K-steps
-    return items <= 1024 && nk >= 32 && nk % 2 == 0 ? 2 : 1;
+    int s = items <= 1024 && nk >= 32 && nk % 2 == 0 ? 2 : 1;
+    while (2 * s <= 8 && items * s < 256 && nk % (2 * s) == 0 && nk / (2 * s) >= 8) s *= 2;
+    return s;
 }
 
 // Lays the workspace out from `base` (nullptr: sizes only).
@@ -89,7 +117,7 @@ static MoeWs ws_layout(const MoeConfig& c, int dtype, uint8_t* base) {
     w.counts = (int*)take(4 * E);
     w.offsets = (int*)take(4 * (E + 1));
     w.num_tiles = (int*)take(4);
-    w.tiles = (int4*)take(16 * (size_t)max_mtiles((long)P, (int)E));
+    w.tiles = (int4*)take(16 * (size_t)max_mtiles((long)P, (int)E, mtile_rows(c, dtype)));
     w.sorted_token = (int*)take(4 * P);
     w.sorted_slot = (int*)take(4 * P);
     w.sorted_w = (float*)take(4 * P);
@@ -173,12 +201,6 @@ static int check_gate_cfg(const MoeConfig* cfg) {
     return check_cfg(&c, AMDMOE_DTYPE_F32);
 }
 
-// fp32 D and I the MFMA kernels tile (whole 32-element K steps); other
-// shapes take the bounds-checked kernels of moe_generic.hip
-static bool f32_mfma_shape(const MoeConfig& c) {
-    return c.hidden_dim % 32 == 0 && c.intermediate_dim % 32 == 0;
-}
-
 static int resolve_ws(const MoeConfig& c, int dtype, void* workspace, size_t bytes, MoeWs* out) {
     MoeWs sz = ws_layout(c, dtype, nullptr);
     void* base = workspace;
@@ -208,12 +230,16 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     const int T = c.num_tokens, E = c.num_experts, K = c.top_k, D = c.hidden_dim,
               I = c.intermediate_dim;
     const long P = (long)T * K;
-    const long mtiles = max_mtiles(P, E);
+    // the MoeConfig dtype of this path (tile rows and K splits are chosen on it)
+    const int cdt = dt == DT_F32 ? AMDMOE_DTYPE_F32
+                                 : (dt == DT_BF16 ? AMDMOE_DTYPE_BF16 : (dt == DT_MX ? AMDMOE_DTYPE_MXFP4 : AMDMOE_DTYPE_FP8));
+    const int bm = mtile_rows(c, cdt);
+    const long mtiles = max_mtiles(P, E, bm);
     const int es = dt == DT_F32 ? 4 : (dt == DT_BF16 ? 2 : 1);  // activation bytes per element
     const int wdiv = dt == DT_MX ? 2 : 1;                       // MX weights: two E2M1 per byte
     // fp8 / MX: with the permutation, x's block scales K-step major in
     // sorted row order (the grouped GEMM's a_scale layout)
-    TRY(launch_permute(w.idx, T, K, E, kMTile, w.counts, w.offsets, w.sorted_token,
+    TRY(launch_permute(w.idx, T, K, E, bm, w.counts, w.offsets, w.sorted_token,
                        w.sorted_slot, w.tiles, w.num_tiles,
                        permute_scratch_bytes(T, E) ? w.perm : nullptr, w.wts, w.sorted_w, st,
                        (const uint32_t*)x_scale, x_scale ? D / 128 : 0, x_scale ? (uint32_t*)w.xs_sorted : nullptr));
@@ -276,8 +302,7 @@ static int moe_experts(int dt, const MoeConfig& c, const MoeWs& w, const uint8_t
     dn.out = w.ypair;
     dn.sorted_slot = w.sorted_slot;
     dn.sorted_w = w.sorted_w;
-    const int nsplit = dt == DT_F32 ? down_splits(c, AMDMOE_DTYPE_F32)
-                                    : (dt == DT_BF16 ? down_splits(c, AMDMOE_DTYPE_BF16) : 1);
+    const int nsplit = down_splits(c, cdt);
     dn.k_splits = nsplit;
     dn.out_split_stride = P * D;
     TRY(launch_grouped_gemm(dt, MODE_DOWN, dn, mtiles, st));

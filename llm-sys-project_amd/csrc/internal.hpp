@@ -105,7 +105,7 @@ int launch_quant_weight(const float* w, long rows, int cols, const float* u, uin
                         float* scale, hipStream_t st);
 
 // moe_gemm.hip
-long max_mtiles(long P, int E);
+long max_mtiles(long P, int E, int BM = kMTile);
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st);
 // moe_gemm_bf16_w4.hip: the bf16 packed-weight GEMMs on one wave per SIMD
 int launch_gemm_bf16_w4(int mode, const GemmArgs& g, long max_tiles, hipStream_t st);

@@ -5,8 +5,8 @@
 namespace amdmoe {
 
 // ---------------------------------------------------------------- launch
-// Upper bound of M-tiles for P routed rows over E experts.
-long max_mtiles(long P, int E) { return P / kBM + (P < E ? P : E); }
+// Upper bound of M-tiles of at most BM rows for P routed rows over E experts.
+long max_mtiles(long P, int E, int BM) { return P / BM + (P < E ? P : E); }
 
 int launch_grouped_gemm(int dt, int mode, const GemmArgs& g, long max_tiles, hipStream_t st) {
     // operands stay below 2 GiB so the out-of-range voffset (2^31) always
