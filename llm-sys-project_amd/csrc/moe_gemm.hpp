@@ -256,24 +256,38 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // ---- activation DMA offsets: wave w fills rows [32w, 32w+32) ----
     const int lrow = lane >> 3;              // row within an 8-row, 1 KB slab
     const int lchunk = (lane & 7) ^ lrow;    // global chunk landing at lane's LDS slot
-    // Prologue loads, issued together so they cost one round trip: the
-    // weight scales of this work item for every K block (fp8; one per
-    // thread, 2 * kb_per_row <= 256 of them, -> LDS before the main loop),
-    // UP's row indices (a_map), and DOWN's slot and routing weight of each
-    // row, which only the epilogue needs: those stay in flight through the
-    // main loop (the barrier below waits for the LDS writes, not for them).
-    // The loads are unconditional, from clamped in-range addresses: in a
-    // branch, each would be waited for on its own.
+    // Prologue loads: the weight scales of this work item for every K block
+    // (fp8: [which][kMaxKb] dwords in LDS, kb < kb_per_row), UP's row
+    // indices (a_map), and DOWN's slot and routing weight of each row, which
+    // only the epilogue needs: those stay in flight through the main loop.
+    // DOWN loads the scales straight into LDS by the LDS DMA of waves 0-3
+    // (lane l of wave w writes dword 64w + l: waves 0-1 fill block 0, waves
+    // 2-3 block 1 at dword kMaxKb = 128), with no register wait: they
+    // are the oldest loads of those waves, so the first K-step's vmcnt wait
+    // and barrier cover them, and the weight ring goes out one round trip
+    // earlier (DSV3 DOWN -0.3% at T=4096, -1.7% at T=8192).  UP waits for
+    // a_map before its ring anyway, so it loads one scale per thread into
+    // registers and then LDS, behind a barrier.  The register loads are
+    // unconditional, from clamped in-range addresses: in a branch, each
+    // would be waited for on its own.
     float sb_val = 0.0f;
     int sb_pos = -1;
-    if (DT == DT_FP8) {
+    if (DT == DT_FP8 && MODE == MODE_UP) {
         const float* bse = g.b_scale + (size_t)e * (g.b_rows / 128) * kb_per_row;
         const int i = min(tid, 2 * kb_per_row - 1);
         const int which = i / kb_per_row, kb = i - which * kb_per_row;
-        const int nb = MODE == MODE_UP ? (which == 0 ? nt : g.n_out / 128 + nt)
-                                       : min(2 * nt + which, g.b_rows / 128 - 1);
+        const int nb = which == 0 ? nt : g.n_out / 128 + nt;
         sb_val = bse[(size_t)nb * kb_per_row + kb];
         sb_pos = tid < 2 * kb_per_row ? which * kMaxKb + kb : -1;
+    }
+    if (DT == DT_FP8 && MODE == MODE_DOWN && wave < 4) {
+        const int nbr = g.b_rows / 128;  // 128-row scale blocks per expert
+        const __amdgpu_buffer_rsrc_t rsb =
+            make_rsrc(g.b_scale + (size_t)e * nbr * kb_per_row, (long)nbr * kb_per_row * 4);
+        const int which = wave >> 1, kb = 64 * (wave & 1) + lane;
+        const int nb = 2 * nt + which;  // waves 0-3 of the loop use block 2nt, waves 4-7 block 2nt + 1
+        const uint32_t vo = kb < kb_per_row && nb < nbr ? (uint32_t)((nb * kb_per_row + kb) * 4) : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (lds_ptr_t)(smem + kBScaleOff + 256 * wave), 4, vo, 0, 0, 0);
     }
     // UP gathers the rows through a_map (index clamped to a live row; the
     // offset of a row past the tile is replaced by the out-of-range one)
@@ -533,8 +547,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         }
     };
 
-    static_assert(2 * kMaxKb <= 512, "one weight-scale load per thread");
-    lds_barrier();  // weight scales in LDS (DOWN's slot / weight loads may still be in flight)
+    static_assert(kMaxKb == 128, "DOWN's scale DMA: two waves of 64 lanes per 128-row block");
+    if (!(DT == DT_FP8 && MODE == MODE_DOWN)) lds_barrier();  // UP's weight scales in LDS
     // Prefetch distances: activations 2 K-steps ahead (a 3-stage LDS ring;
     // they come from L2), weights RB-1 K-steps ahead in a ring of RB
     // register sets -- as deep as the registers left by the live
