@@ -48,8 +48,7 @@
 // per live token-tile count), so they compile in parallel.  Built: fp8 and
 // MX (both projections), fp32.  The bf16 GEMMs run
 // grouped_gemm_bf16_w4_kernel (moe_gemm_bf16_w4.hip: same items and
-// arithmetic, 4 waves x 64 weight rows); the template's bf16 branches are
-// not instantiated.
+// arithmetic, 4 waves x 64 weight rows); this template has no bf16 form.
 #pragma once
 
 #include <type_traits>
@@ -88,7 +87,6 @@ static_assert(128 * 528 <= kNS * kStageBytes, "DOWN epilogue staging fits the ri
 
 template <int DT> struct DtTraits;
 template <> struct DtTraits<DT_F32> { static constexpr int es = 4; };
-template <> struct DtTraits<DT_BF16> { static constexpr int es = 2; };
 template <> struct DtTraits<DT_FP8> { static constexpr int es = 1; };
 template <> struct DtTraits<DT_MX> { static constexpr int es = 1; };  // activation bytes per element
 
@@ -199,6 +197,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // loads into registers (MX: per column tile 16 bytes of E2M1 and one
     // scale byte); a wave whose activation rows are all past the live token
     // tiles issues only the weight loads
+    static_assert(DT != DT_BF16, "the bf16 GEMMs are grouped_gemm_bf16_w4_kernel");
     constexpr bool kScaledA = DT == DT_FP8 || DT == DT_MX;  // activations carry row scales
     static_assert(DT != DT_MX || PK, "MX weights exist in fragment order only");
     using Frag = std::conditional_t<DT == DT_MX, BFragMx, BFrag>;
@@ -213,7 +212,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
     // ---- work item (XCD-chunked) ----
     // DOWN with fp32 rows may split K over S items per (M-tile, N-tile):
     // virtual N-tile v = S * nt + ks (uniform)
-    constexpr bool kCanSplit = MODE == MODE_DOWN && (DT == DT_F32 || DT == DT_BF16);
+    constexpr bool kCanSplit = MODE == MODE_DOWN && DT == DT_F32;
     const int S = kCanSplit ? max(g.k_splits, 1) : 1;
     const int W = (*g.num_tiles) * g.n_tiles_n * S;
     const int per = (W + 7) >> 3;
@@ -478,16 +477,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
             } else {
 #pragma unroll
                 for (int ct = 0; ct < 2; ct++) {
-                    const u32x4 wlo = bf.q[ct][0], whi = bf.q[ct][1];  // f32 / bf16
-                    if (DT == DT_F32) {
-                        for (int j = 0; j < 4; j++)
-                            acc[rt][ct] = mfma_f32(__uint_as_float(wlo[j]), __uint_as_float(xlo[j]), acc[rt][ct]);
-                        for (int j = 0; j < 4; j++)
-                            acc[rt][ct] = mfma_f32(__uint_as_float(whi[j]), __uint_as_float(xhi[j]), acc[rt][ct]);
-                    } else {
-                        acc[rt][ct] = mfma_bf16(wlo, xlo, acc[rt][ct]);
-                        acc[rt][ct] = mfma_bf16(whi, xhi, acc[rt][ct]);
-                    }
+                    const u32x4 wlo = bf.q[ct][0], whi = bf.q[ct][1];  // f32
+                    for (int j = 0; j < 4; j++)
+                        acc[rt][ct] = mfma_f32(__uint_as_float(wlo[j]), __uint_as_float(xlo[j]), acc[rt][ct]);
+                    for (int j = 0; j < 4; j++)
+                        acc[rt][ct] = mfma_f32(__uint_as_float(whi[j]), __uint_as_float(xhi[j]), acc[rt][ct]);
                 }
             }
             // pin the products here: without it the MFMAs float to their
@@ -735,8 +729,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
 #undef SLOT_ARGS
     // The loop is instantiated per live token-tile count: fp8 and MX (the
     // layer's headline paths, where an expert's 128 +- 11 rows would
-    // otherwise be rounded up to 192) in steps of one 16-row tile, the fp32 /
-    // bf16 paths in groups of four.
+    // otherwise be rounded up to 192) in steps of one 16-row tile, the fp32
+    // path in groups of four.
     const int ntiles = (rows + 15) / 16;  // 1..16, uniform
     if constexpr (kScaledA) {
         static_for<16>([&](auto ic) __attribute__((always_inline)) {
@@ -779,8 +773,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                         hv[i] = gv * uv * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gv));
                     } else {
                         // fp32 keeps the reference's expf and IEEE division
-                        // (naive_moe.cu:297-310); bf16 / MX use the hardware
-                        // exp2 and reciprocal (~1 ulp each)
+                        // (naive_moe.cu:297-310); MX uses the hardware exp2
+                        // and reciprocal (~1 ulp each)
                         const float silu = DT == DT_F32 ? gv / (1.0f + expf(-gv))
                                                         : gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
                         hv[i] = silu * uv;
@@ -860,15 +854,6 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
                     ((uint8_t*)g.out_scale)[((size_t)(col / 128) * g.out_scale_rows + pos) * 4 + (col / 32) % 4] =
                         (uint8_t)e8;
                 }
-            } else if (DT == DT_BF16) {
-                if (ok) {
-                    uint8_t* dst = g.out + (pos * g.n_out + col) * 2;
-                    for (int k = 0; k < 4; k++) {
-                        u32x4 o;
-                        for (int m = 0; m < 4; m++) o[m] = pack_bf16x2(v[8 * k + 2 * m], v[8 * k + 2 * m + 1]);
-                        *(u32x4*)(dst + 16 * ((k + 2 * rot) & 3)) = o;
-                    }
-                }
             } else {
                 if (ok) {
                     float* dst = (float*)g.out + pos * g.n_out + col;
@@ -884,10 +869,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(GemmArgs g) {
         // LDS (staged in the prologue)
         const int* s_slot = (const int*)(smem + kRowInfoOff);
         const float* s_wt = (const float*)(smem + kRowInfoOff) + kBM;
-        if (DT == DT_F32 || DT == DT_BF16) {
-            // fp32 rows (the reference path, and the bf16 layer, whose output
-            // is then rounded once, in the combine): 16-byte stores straight
-            // from the accumulators
+        if (DT == DT_F32) {
+            // fp32 rows (the fp32 layer, the reference's format): 16-byte
+            // stores straight from the accumulators
 #pragma unroll
             for (int rt = 0; rt < 16; rt++) {
                 if (16 * rt >= rows) continue;  // uniform; unrolled so acc[] stays in registers
@@ -958,7 +942,7 @@ int launch_gemm_variant(const GemmArgs& g, long max_tiles, hipStream_t st) {
         const int rc = ensure_dynamic_lds((const void*)grouped_gemm_kernel<DT, MODE, PK>, kGemmLds);
         if (rc != AMDMOE_OK) return rc;
     }
-    long work = max_tiles * g.n_tiles_n * (MODE == MODE_DOWN && (DT == DT_F32 || DT == DT_BF16) ? max(g.k_splits, 1) : 1);
+    long work = max_tiles * g.n_tiles_n * (MODE == MODE_DOWN && DT == DT_F32 ? max(g.k_splits, 1) : 1);
     long grid = 8 * ceil_div(work, 8);
     if (grid == 0) return AMDMOE_OK;
     AMDMOE_CHECK_ARG(grid < (1L << 31), "grouped gemm: grid too large (%ld)", grid);
