@@ -348,8 +348,11 @@ def test_forward_f32_reference_cases(amd, orc, name, shape, tol):
 @pytest.mark.parametrize("T,E,K,D,I", [(1024, 4, 2, 128, 256), (512, 4, 2, 64, 128),
                                        (600, 3, 2, 64, 128)])
 def test_forward_f32_multi_mtile_experts(amd, orc, T, E, K, D, I):
-    """Experts of 2-3 M-tiles and of 1-2 M-tiles (a full 256-row tile plus
-    a small one), on the reference's inputs, at the fp32 bar."""
+    """Experts of several M-tiles, on the reference's inputs, at the fp32 bar.
+    These small layers get 64-row M-tiles (too few UP work items for 256-row
+    ones), so an expert of ~256-512 rows splits into 4-8 balanced tiles;
+    256-row tiles with a small remainder tile are covered by
+    test_forward_every_tile_group_f32_bf16 at I = 2048."""
     announce(f"forward_f32 multi-M-tile experts {(T, E, K, D, I)}")
     x, wg, w1, w2 = orc.reference_moe_inputs(T, E, K, D, I)
     _, _, y_ref = orc.moe_forward_f32(x, wg, w1, w2, K)
