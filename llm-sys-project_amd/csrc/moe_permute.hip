@@ -368,35 +368,35 @@ __global__ __launch_bounds__(kFusedThreads) void perm_scan_scatter_kernel(
         offsets[E] = ar;
         *num_tiles = at;
     }
-    // this block's 64 tokens: lane masks per expert, then every first
-    // occurrence goes to its row
+    // this block's 64 tokens: lane masks per expert (bit i = token i of the
+    // block), then every first occurrence goes to its row -- one thread per
+    // (token, slot) pair, token = lane and slot k = wave (+16 per pass for
+    // K > 16): the expert's offset plus the block's earlier tokens in it
     for (int e = tid; e < E; e += kFusedThreads) s_mask[e] = 0ull;
     __syncthreads();
     const int t = b * kPermTok + lane;
     const int* row = idx + (size_t)t * K;
-    if (wave == 0 && t < T) {
-        for (int k = 0; k < K; k++) {
-            const int v = row[k];
-            if (v < 0 || v >= E) continue;
-            bool dup = false;
-            for (int j = 0; j < k; j++) dup |= row[j] == v;
-            if (!dup) atomicOr(&s_mask[v], 1ull << lane);
-        }
+    for (int k = wave; k < K; k += kFusedThreads / 64) {
+        if (t >= T) break;
+        const int v = row[k];
+        if (v < 0 || v >= E) continue;
+        bool dup = false;
+        for (int j = 0; j < k; j++) dup |= row[j] == v;
+        if (!dup) atomicOr(&s_mask[v], 1ull << lane);
     }
     __syncthreads();
-    if (wave == 0 && t < T) {
-        const unsigned long long below = (1ull << lane) - 1ull;
-        for (int k = 0; k < K; k++) {
-            const int v = row[k];
-            if (v < 0 || v >= E) continue;
-            bool dup = false;
-            for (int j = 0; j < k; j++) dup |= row[j] == v;
-            if (dup) continue;
-            const int pos = s_off[v] + __popcll(s_mask[v] & below);
-            sorted_token[pos] = t;
-            sorted_slot[pos] = t * K + k;
-            if (sorted_w) sorted_w[pos] = wts[(size_t)t * K + k];
-        }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int k = wave; k < K; k += kFusedThreads / 64) {
+        if (t >= T) break;
+        const int v = row[k];
+        if (v < 0 || v >= E) continue;
+        bool dup = false;
+        for (int j = 0; j < k; j++) dup |= row[j] == v;
+        if (dup) continue;
+        const int pos = s_off[v] + __popcll(s_mask[v] & below);
+        sorted_token[pos] = t;
+        sorted_slot[pos] = t * K + k;
+        if (sorted_w) sorted_w[pos] = wts[(size_t)t * K + k];
     }
 }
 
