@@ -602,23 +602,27 @@ int launch_gather_one(const float* x, const int* idx, int T, int K, int E, int D
 // as 16-byte vectors where aligned) go to nkb K-step rows of dst, so each
 // K-step row is written coalesced across the wave.  Rows past the valid
 // ones (sorted_token not written there) read token 0: never consumed.
+// One thread per (sorted row p, group of G scales): p runs fastest, so a
+// wave's stores for one scale block are 64 consecutive dwords; G = 4 (one
+// 16-byte load) when nkb is a multiple of 4, else 1.  Every row's gathers
+// spread over nkb / G threads, all loads of a thread in one round trip.
+template <int G>
 __global__ __launch_bounds__(256) void gather_row_scales_kernel(const uint32_t* __restrict__ src,
                                                                 const int* __restrict__ sorted_token,
                                                                 long P, int T, int nkb,
                                                                 uint32_t* __restrict__ dst) {
-    const long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= P) return;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long g = i / P, p = i - g * P;  // scale group, sorted row
+    if (g * G >= nkb) return;
     int t = sorted_token[p];
     t = (t >= 0 && t < T) ? t : 0;
-    const uint32_t* row = src + (size_t)t * nkb;
-    if ((nkb & 3) == 0) {
-        for (int kb = 0; kb < nkb; kb += 4) {
-            const u32x4 v = *(const u32x4*)(row + kb);
+    const uint32_t* row = src + (size_t)t * nkb + g * G;
+    if constexpr (G == 4) {
+        const u32x4 v = *(const u32x4*)row;
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[(size_t)(kb + i) * P + p] = v[i];
-        }
+        for (int k = 0; k < 4; k++) dst[(size_t)(4 * g + k) * P + p] = v[k];
     } else {
-        for (int kb = 0; kb < nkb; kb++) dst[(size_t)kb * P + p] = row[kb];
+        dst[(size_t)g * P + p] = *row;
     }
 }
 
@@ -626,8 +630,15 @@ int launch_gather_row_scales(const uint32_t* src, const int* sorted_token, long 
                              uint32_t* dst, hipStream_t st) {
     AMDMOE_CHECK_ARG(P >= 0 && T > 0 && nkb > 0, "gather_row_scales: P=%ld T=%d nkb=%d", P, T, nkb);
     if (P == 0) return AMDMOE_OK;
-    hipLaunchKernelGGL(gather_row_scales_kernel, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, st, src,
-                       sorted_token, P, T, nkb, dst);
+    const bool vec = (nkb & 3) == 0;
+    const long threads = P * (vec ? nkb / 4 : nkb);
+    AMDMOE_CHECK_ARG(ceil_div(threads, 256) < (1L << 31), "gather_row_scales: %ld threads", threads);
+    if (vec)
+        hipLaunchKernelGGL(gather_row_scales_kernel<4>, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st,
+                           src, sorted_token, P, T, nkb, dst);
+    else
+        hipLaunchKernelGGL(gather_row_scales_kernel<1>, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, st,
+                           src, sorted_token, P, T, nkb, dst);
     AMDMOE_LAUNCH_CHECK();
     return AMDMOE_OK;
 }
