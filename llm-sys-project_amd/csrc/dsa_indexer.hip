@@ -199,6 +199,37 @@ __device__ __forceinline__ int count_below(unsigned long long m) {
     return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
 }
 
+// x shifted across the lanes of each 16-lane row with DPP (row_shl:n reads
+// lane + n, row_shr:n lane - n), 0 where the source lane leaves the row
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_row(unsigned x) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// inclusive sums over the wave: of this lane and every higher lane (suffix)
+// or every lower lane (prefix).  Four DPP steps within each row, then the
+// totals of the other rows (read from one lane of each) -- no LDS round
+// trips, where a shuffle scan takes six.
+__device__ __forceinline__ unsigned wave_suffix_sum(unsigned x, int lane) {
+    x += dpp_row<0x101>(x);
+    x += dpp_row<0x102>(x);
+    x += dpp_row<0x104>(x);
+    x += dpp_row<0x108>(x);
+    const unsigned t1 = __builtin_amdgcn_readlane(x, 16), t2 = __builtin_amdgcn_readlane(x, 32),
+                   t3 = __builtin_amdgcn_readlane(x, 48);
+    const int row = lane >> 4;
+    return x + (row < 1 ? t1 : 0u) + (row < 2 ? t2 : 0u) + (row < 3 ? t3 : 0u);
+}
+__device__ __forceinline__ unsigned wave_prefix_sum(unsigned x, int lane) {
+    x += dpp_row<0x111>(x);
+    x += dpp_row<0x112>(x);
+    x += dpp_row<0x114>(x);
+    x += dpp_row<0x118>(x);
+    const unsigned t0 = __builtin_amdgcn_readlane(x, 15), t1 = __builtin_amdgcn_readlane(x, 31),
+                   t2 = __builtin_amdgcn_readlane(x, 47);
+    const int row = lane >> 4;
+    return x + (row > 0 ? t0 : 0u) + (row > 1 ? t1 : 0u) + (row > 2 ? t2 : 0u);
+}
+
 // Selection modes: FULL selects a query's row in one workgroup; PART
 // selects within one of the row's parts (positions [part * chunk, +chunk))
 // and writes its top-k as (key, position) candidates in position order,
@@ -304,20 +335,13 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
                 // count of keys with digit >= 4l + i: this lane's suffix plus
                 // every higher lane's total
                 const int s3 = c[3], s2 = s3 + c[2], s1 = s2 + c[1], s0 = s1 + c[0];
-                int x = s0;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int y = __shfl_down(x, o, 64);
-                    if (lane + o < 64) x += y;
-                }
-                const int above = x - s0;
+                const int above = (int)wave_suffix_sum((unsigned)s0, lane) - s0;
                 const int ge[4] = {above + s0, above + s1, above + s2, above + s3};
                 // the digit is the largest d whose count of keys >= d reaches
                 // need; the counts fall with d, so it is the number of such
                 // digits minus one (digit 0 if none)
-                int cnt = (ge[0] >= need) + (ge[1] >= need) + (ge[2] >= need) + (ge[3] >= need);
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) cnt += __shfl_xor(cnt, o, 64);
+                const int cnt = __popcll(__ballot(ge[0] >= need)) + __popcll(__ballot(ge[1] >= need)) +
+                                __popcll(__ballot(ge[2] >= need)) + __popcll(__ballot(ge[3] >= need));
                 const int d = max(cnt - 1, 0);
                 if (lane == (d >> 2)) {
                     const int i = d & 3;
@@ -361,12 +385,7 @@ __global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const float*
                 s_cnt[w * kPer + lane] = run;
                 run += v;
             }
-        unsigned x = run;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const unsigned y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
+        const unsigned x = wave_prefix_sum(run, lane);
         if (lane < kPer) s_slice[lane] = x - run;
         if (lane == kPer - 1) s_slice[kPer] = x;
     }
