@@ -475,7 +475,7 @@ def traffic_summary(fetch_dir, write_dir, out_md, out_json, command,
     f_write = per_dispatch_kib / wa[c]["WRITE_SIZE"]
     rows, kernels = [], {}
     for k in sorted(fa, key=lambda k: -fa[k]["FETCH_SIZE"]):
-        if k.startswith("at::") or k.startswith("rocprim") or k not in wa or k == c:
+        if not k or k.startswith("at::") or k.startswith("rocprim") or k not in wa or k == c:
             continue
         fb = fa[k]["FETCH_SIZE"] * 1024 * f_fetch
         wb = wa[k]["WRITE_SIZE"] * 1024 * f_write
